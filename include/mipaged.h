@@ -1,0 +1,137 @@
+/*
+ * mipaged.h — C ABI of the MI355X paged KV-cache kernels (gfx950).
+ *
+ * Three operations sit behind this boundary:
+ *   1. KV append          : scatter new K/V rows into the paged pool through a slot mapping.
+ *   2. Paged decode attn  : one query token per sequence, GQA, reading K/V pages in place
+ *                           through per-sequence block tables.
+ *   3. Block copy         : copy whole blocks (all layers, K and V) for copy-on-write of
+ *                           shared prefix blocks.
+ *
+ * Pool layout (one layer; identical to the reference pool
+ * engine/kv_cache.py:426-428, `k, v: [num_layers, num_blocks + 1, num_kv_heads,
+ * block_size, head_dim]`, the extra block being the scratch block):
+ *
+ *     cache[block][kv_head][offset][d]     d contiguous, element type = dtype
+ *
+ * so the (block, kv_head) tile of block_size * head_dim elements is one contiguous run.
+ * A slot is the flat token index  slot = block * block_size + offset.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers owned by the caller; nothing here allocates,
+ *     frees or synchronises. Work is enqueued on `stream` (a hipStream_t; NULL = the
+ *     null stream) and the call returns immediately.
+ *   - Strides are in ELEMENTS, not bytes. The last (head_dim) dimension must be
+ *     contiguous.
+ *   - Return value: MIP_OK (0) on success, MIP_EINVAL (-22) for arguments that fail the
+ *     host-side checks (nothing is launched), MIP_EUNSUPPORTED (-95) for a shape with no
+ *     compiled kernel, or a positive hipError_t from the launch.
+ *   - Calls are asynchronous and graph-capturable: the grid depends only on the integer
+ *     arguments, never on device data.
+ */
+#ifndef MIPAGED_H_
+#define MIPAGED_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum mip_dtype { MIP_F32 = 0, MIP_F16 = 1, MIP_BF16 = 2 };
+
+enum mip_status { MIP_OK = 0, MIP_EINVAL = -22, MIP_EUNSUPPORTED = -95 };
+
+/* Library version, (major << 16) | minor. */
+int mip_version(void);
+
+/* Human-readable text for a status code returned by any entry point. */
+const char* mip_status_string(int status);
+
+/*
+ * KV append.
+ *
+ * Replaces the scatter in PagedDecodeContext.attend
+ *   engine/kv_cache.py:613-614   k_layer[write_blocks, :, write_offsets] = k[:, :, 0]
+ * and the packed-prefill scatter in PackedPrefillContext.attend
+ *   engine/kv_cache.py:286-289   k_layer[where_0, :, where_2] = k[0].transpose(0, 1)
+ * (and the same writes inside the graphed decode, engine/cuda_graphs.py:82-83).
+ *
+ * Token i (0 <= i < n_tokens), kv head h: the head_dim elements at
+ *     k_src + i * k_stride_tok + h * k_stride_head
+ * are copied bit for bit to row ((s / block_size) * num_kv_heads + h) * block_size
+ * + s % block_size of k_cache, where s = slot_mapping[i]; likewise for V.
+ * A slot outside [0, num_cache_blocks * block_size) is skipped (write nothing), so
+ * negative slots can mark padding rows. Slots must be distinct (as for index_put_
+ * without accumulate, duplicate targets leave an unspecified winner).
+ */
+int mip_kv_append(const void* k_src, const void* v_src,
+                  int64_t k_stride_tok, int64_t k_stride_head,
+                  int64_t v_stride_tok, int64_t v_stride_head,
+                  void* k_cache, void* v_cache, int64_t num_cache_blocks,
+                  const int64_t* slot_mapping, int32_t n_tokens,
+                  int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                  int32_t dtype, void* stream);
+
+/*
+ * Paged decode attention (one new token per sequence, GQA).
+ *
+ * Replaces the gather + SDPA of PagedDecodeContext.attend
+ *   engine/kv_cache.py:615-620   keys = k_layer[tables].permute(0, 2, 1, 3, 4).reshape(...)
+ *                                 decode_attention(q, keys, values, attn_mask=mask)
+ * and engine/model.py:126-147 (decode_attention: query head h reads kv head
+ * h / (num_heads / num_kv_heads)), with the mask `arange(kv_len) <= positions`
+ * (engine/kv_cache.py:609) expressed as context_lens[b] = positions[b] + 1.
+ *
+ *   out[b, h, :] = softmax_j( scale * q[b, h, :] . K_b[j, :] ) @ V_b[j, :],
+ *                  j < context_lens[b],
+ *   K_b[j] = k_cache row (block_tables[b * bt_stride + j / block_size], h / group, j % block_size)
+ *
+ * Arithmetic: products and sums in fp32, output rounded once to dtype.
+ * Entries of a block table past ceil(context_lens[b] / block_size) are never read.
+ * A sequence with context_lens[b] <= 0 gets a zero output row.
+ * context_lens[b] must not exceed max_blocks_per_seq * block_size (larger values are
+ * clamped to it).
+ *
+ * `workspace` must hold mip_paged_decode_workspace(...) bytes for the same shape, be
+ * 256-byte aligned and be zero-filled ONCE when first allocated: the kernel leaves its
+ * counters at zero again when it finishes, so the buffer can be reused by later calls
+ * on the same stream without clearing. Two calls that run concurrently must not share
+ * a workspace.
+ */
+int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h,
+                     const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
+                     const int32_t* block_tables, int64_t bt_stride,
+                     const int32_t* context_lens,
+                     int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
+                     float scale, void* workspace, size_t workspace_bytes,
+                     int32_t dtype, void* stream);
+
+/* Workspace bytes mip_paged_decode needs for this shape (0 when it needs none). */
+size_t mip_paged_decode_workspace(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t block_size,
+                                  int32_t max_blocks_per_seq, int32_t dtype);
+
+/*
+ * Block copy for copy-on-write of shared prefix blocks.
+ *
+ * No reference counterpart: the reference shares only full, never-rewritten prefix
+ * blocks (engine/kv_cache.py:499-508, 527). The operation is the bitwise
+ *     k[l, dst] = k[l, src];  v[l, dst] = v[l, src]     for every layer l
+ * over a pool laid out [num_layers][num_cache_blocks][block_bytes].
+ * `pairs` is int64 [n_pairs][2] = (src, dst). Pairs with an index outside
+ * [0, num_cache_blocks) are skipped. Destinations must be distinct and must not be
+ * the source of another pair in the same call.
+ */
+int mip_copy_blocks(void* k_cache, void* v_cache, const int64_t* pairs, int32_t n_pairs,
+                    int32_t num_layers, int64_t num_cache_blocks, int64_t block_bytes,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIPAGED_H_ */

@@ -1,0 +1,80 @@
+"""ctypes binding of libmipaged.so, the C-ABI HIP library (declared in include/mipaged.h).
+
+Loading is lazy and strict: any use of a kernel without the built library, or with
+tensors that are not on a ROCm device, raises. There is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmipaged.so"
+
+MIP_F32, MIP_F16, MIP_BF16 = 0, 1, 2
+MIP_OK, MIP_EINVAL, MIP_EUNSUPPORTED = 0, -22, -95
+
+EXPORTED = (
+    "mip_version",
+    "mip_status_string",
+    "mip_kv_append",
+    "mip_paged_decode",
+    "mip_paged_decode_workspace",
+    "mip_copy_blocks",
+)
+
+_c = ctypes
+_i32, _i64, _sz, _vp, _f32 = _c.c_int32, _c.c_int64, _c.c_size_t, _c.c_void_p, _c.c_float
+
+_SIGNATURES = {
+    "mip_version": (_c.c_int, []),
+    "mip_status_string": (_c.c_char_p, [_c.c_int]),
+    "mip_kv_append": (
+        _c.c_int,
+        [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "mip_paged_decode": (
+        _c.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
+         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _i32, _vp],
+    ),
+    "mip_paged_decode_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "mip_copy_blocks": (_c.c_int, [_vp, _vp, _vp, _i32, _i32, _i64, _i64, _vp]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load (once) and return the library, with argument types set for every entry point."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise NativeLibraryMissing(
+            f"{p} is not built; run `python mini-inference_amd/build.py` (or __graft_entry__.build())"
+        )
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != MIP_OK:
+        msg = load().mip_status_string(status).decode()
+        raise NativeError(f"{what} failed: status {status} ({msg})")

@@ -1,0 +1,388 @@
+"""Paged KV cache whose attention contexts run the MI355X HIP kernels.
+
+Drop-in for the paged half of the reference's engine/kv_cache.py:
+
+* :class:`PagedKVCache` keeps the reference's pool tensors, public state and allocator
+  API (engine/kv_cache.py:377-579) with the same block-reuse policy, so the scheduler,
+  prefix caching and graph code see the same block ids. It adds :meth:`copy_blocks`
+  and :meth:`fork` for copy-on-write of shared blocks.
+* :class:`PagedDecodeContext` (engine/kv_cache.py:582-624): ``attend`` = KV append
+  kernel + paged decode-attention kernel. No gathered copy of the history is made.
+* :class:`PackedPrefillContext` (engine/kv_cache.py:218-301): the packed scatter is the
+  append kernel; the prefill attention itself stays in torch SDPA.
+
+Pool layout (reference engine/kv_cache.py:426-428):
+``k, v: [num_layers, num_blocks + 1, num_kv_heads, block_size, head_dim]``; block
+``num_blocks`` is the scratch block that graph padding rows point at.
+"""
+
+from __future__ import annotations
+
+from collections import OrderedDict
+from collections.abc import Sequence
+
+import numpy as np
+import torch
+
+from . import paged_ops
+from .model import Qwen2Config, sdpa_attention
+
+
+class PagedKVCache:
+    """Fixed-size blocks handed out to sequences; optional content-keyed prefix sharing.
+
+    A sequence ("slot") owns a block table: token p lives in block ``table[p // block_size]``
+    at offset ``p % block_size``. Block reuse order, reference counting and prefix keys
+    follow engine/kv_cache.py:436-560 exactly:
+
+    * free blocks form an LRU queue, least recently freed first; a released block that
+      holds no cached prefix is put at the head so it is reused before cached ones;
+    * a full block is keyed by ``(hash(previous key), its tokens)``; registered blocks
+      stay findable while free until the queue hands them out again.
+    """
+
+    def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, num_blocks: int, block_size: int,
+                 max_seqs: int, max_len: int, dtype: torch.dtype, device: torch.device | str,
+                 enable_prefix_caching: bool = False) -> None:
+        if block_size <= 0 or block_size & (block_size - 1):
+            raise ValueError(f"block_size must be a power of two, got {block_size}")
+        shape = (num_layers, num_blocks + 1, num_kv_heads, block_size, head_dim)
+        self.k = torch.zeros(shape, dtype=dtype, device=device)
+        self.v = torch.zeros(shape, dtype=dtype, device=device)
+        self.num_layers = num_layers
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.num_blocks = num_blocks
+        self.scratch_block = num_blocks
+        self.block_size = block_size
+        self.max_len = max_len
+        self.enable_prefix_caching = enable_prefix_caching
+        self.lengths: dict[int, int] = {}
+        self.block_tables: dict[int, list[int]] = {}
+        self._free_ids = list(range(max_seqs - 1, -1, -1))  # pop() hands out slot 0 first
+        self._free_blocks: OrderedDict[int, None] = OrderedDict.fromkeys(range(num_blocks))
+        self._ref_counts = [0] * num_blocks
+        self._block_key: dict[int, tuple] = {}
+        self._cached: dict[tuple, int] = {}
+        self.prefix_hit_tokens = 0
+        self.cow_copies = 0  # blocks copied on write so far
+
+    @classmethod
+    def for_model(cls, cfg: Qwen2Config, num_blocks: int, block_size: int, max_seqs: int, max_len: int,
+                  dtype: torch.dtype, device: torch.device | str, enable_prefix_caching: bool = False) -> "PagedKVCache":
+        return cls(cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, num_blocks, block_size, max_seqs, max_len, dtype,
+                   device, enable_prefix_caching)
+
+    # ----------------------------------------------------------------- capacity queries
+    @property
+    def num_free_slots(self) -> int:
+        return len(self._free_ids)
+
+    @property
+    def num_free_blocks(self) -> int:
+        return len(self._free_blocks)
+
+    def blocks_for(self, num_tokens: int) -> int:
+        return (num_tokens + self.block_size - 1) // self.block_size
+
+    def can_allocate(self, num_tokens: int) -> bool:
+        # Same conservative test as the reference: blocks a prefix hit would share are not counted.
+        return (len(self._free_ids) > 0 and num_tokens <= self.max_len
+                and self.blocks_for(num_tokens) <= len(self._free_blocks))
+
+    # ----------------------------------------------------------------- block life cycle
+    def _new_block(self) -> int:
+        block = next(iter(self._free_blocks))
+        del self._free_blocks[block]
+        key = self._block_key.pop(block, None)
+        if key is not None:
+            del self._cached[key]  # its cached prefix is overwritten from now on
+        self._ref_counts[block] = 1
+        return block
+
+    def _share(self, block: int) -> None:
+        if self._ref_counts[block] == 0:
+            del self._free_blocks[block]  # free but still cached: back in use
+        self._ref_counts[block] += 1
+
+    def _release(self, block: int) -> None:
+        self._ref_counts[block] -= 1
+        if self._ref_counts[block]:
+            return
+        self._free_blocks[block] = None  # newest free block: reused last ...
+        if block not in self._block_key:
+            self._free_blocks.move_to_end(block, last=False)  # ... unless it caches nothing
+
+    @staticmethod
+    def _chain_keys(token_ids: Sequence[int], block_size: int, count: int):
+        parent = None
+        for i in range(count):
+            key = (parent, tuple(token_ids[i * block_size:(i + 1) * block_size]))
+            yield key
+            parent = hash(key)
+
+    def _match_prefix(self, token_ids: Sequence[int]) -> list[int]:
+        usable = (len(token_ids) - 1) // self.block_size  # at least one token is always computed
+        found = []
+        for key in self._chain_keys(token_ids, self.block_size, usable):
+            block = self._cached.get(key)
+            if block is None:
+                break
+            found.append(block)
+        return found
+
+    # ----------------------------------------------------------------- sequences
+    def allocate(self, num_tokens: int = 0, token_ids: Sequence[int] | None = None) -> int:
+        if not self.can_allocate(num_tokens):
+            raise RuntimeError("not enough free KV cache blocks")
+        shared = self._match_prefix(token_ids) if (self.enable_prefix_caching and token_ids) else []
+        for block in shared:
+            self._share(block)
+        slot = self._free_ids.pop()
+        fresh = [self._new_block() for _ in range(self.blocks_for(num_tokens) - len(shared))]
+        self.block_tables[slot] = shared + fresh
+        self.lengths[slot] = len(shared) * self.block_size
+        self.prefix_hit_tokens += self.lengths[slot]
+        return slot
+
+    def register_prefix(self, slot: int, token_ids: Sequence[int]) -> None:
+        if not self.enable_prefix_caching:
+            return
+        table = self.block_tables[slot]
+        full = self.lengths[slot] // self.block_size
+        for i, key in enumerate(self._chain_keys(token_ids, self.block_size, full)):
+            if key not in self._cached and table[i] not in self._block_key:
+                self._cached[key] = table[i]
+                self._block_key[table[i]] = key
+
+    def ensure_capacity(self, slot: int, num_tokens: int) -> bool:
+        if num_tokens > self.max_len:
+            return False
+        table = self.block_tables[slot]
+        missing = self.blocks_for(num_tokens) - len(table)
+        if missing > len(self._free_blocks):
+            return False
+        for _ in range(missing):
+            table.append(self._new_block())
+        return True
+
+    def free(self, slot: int) -> None:
+        if slot not in self.block_tables:
+            raise RuntimeError(f"slot {slot} freed twice")
+        for block in reversed(self.block_tables.pop(slot)):
+            self._release(block)
+        del self.lengths[slot]
+        self._free_ids.append(slot)
+
+    def fork(self, slot: int) -> int:
+        """New sequence sharing every block (and the length) of ``slot``.
+
+        Shared blocks are reference counted; the first write into a shared, partially
+        filled block copies it first (see :meth:`prepare_writes`). No reference
+        counterpart: the reference only shares full prefix blocks.
+        """
+        if not self._free_ids:
+            raise RuntimeError("no free sequence slot")
+        table = self.block_tables[slot]
+        for block in table:
+            self._share(block)
+        child = self._free_ids.pop()
+        self.block_tables[child] = list(table)
+        self.lengths[child] = self.lengths[slot]
+        return child
+
+    def ref_count(self, block: int) -> int:
+        return self._ref_counts[block]
+
+    def prepare_writes(self, slots: Sequence[int], starts: Sequence[int], counts: Sequence[int]) -> list[tuple[int, int]]:
+        """Copy-on-write: give every sequence private copies of the shared blocks it is about to write.
+
+        For each sequence, every block touched by tokens ``[start, start + count)`` whose
+        reference count is above one is replaced in that sequence's table by a fresh block,
+        and one :meth:`copy_blocks` launch copies all of them (all layers, K and V).
+        Returns the ``(src, dst)`` pairs copied. Raises if the pool cannot supply them.
+        """
+        pairs: list[tuple[int, int]] = []
+        for slot, start, n in zip(slots, starts, counts):
+            if n <= 0:
+                continue
+            table = self.block_tables[slot]
+            last = min((start + n - 1) // self.block_size, len(table) - 1)
+            for i in range(start // self.block_size, last + 1):
+                old = table[i]
+                if self._ref_counts[old] > 1:
+                    if not self._free_blocks:
+                        raise RuntimeError("not enough free KV cache blocks for copy-on-write")
+                    new = self._new_block()
+                    table[i] = new
+                    self._release(old)
+                    pairs.append((old, new))
+        if pairs:
+            self.copy_blocks(pairs)
+            self.cow_copies += len(pairs)
+        return pairs
+
+    def copy_blocks(self, pairs: Sequence[tuple[int, int]] | torch.Tensor) -> None:
+        """``k[:, dst] = k[:, src]`` and ``v[:, dst] = v[:, src]`` for every (src, dst), all layers, on device."""
+        if isinstance(pairs, torch.Tensor):
+            t = pairs.to(device=self.k.device, dtype=torch.int64).reshape(-1, 2).contiguous()
+        else:
+            if len(pairs) == 0:
+                return
+            t = torch.from_numpy(np.asarray(pairs, dtype=np.int64).reshape(-1, 2)).to(self.k.device)
+        paged_ops.copy_blocks(self.k, self.v, t)
+
+    # ----------------------------------------------------------------- index helpers
+    def write_index(self, slots: Sequence[int], starts: Sequence[int],
+                    counts: Sequence[int]) -> tuple[torch.Tensor, torch.Tensor]:
+        """``(block, offset)`` of tokens ``start .. start+count-1`` of each sequence (kv_cache.py:562-573)."""
+        blocks, offsets = self._write_index_np(slots, starts, counts)
+        return torch.from_numpy(blocks).to(self.k.device), torch.from_numpy(offsets).to(self.k.device)
+
+    def _write_index_np(self, slots, starts, counts) -> tuple[np.ndarray, np.ndarray]:
+        parts_b, parts_o = [], []
+        for slot, a, n in zip(slots, starts, counts):
+            pos = np.arange(a, a + n, dtype=np.int64)
+            table = np.asarray(self.block_tables[slot], dtype=np.int64)
+            parts_b.append(table[pos // self.block_size])
+            parts_o.append(pos % self.block_size)
+        if not parts_b:
+            return np.zeros(0, np.int64), np.zeros(0, np.int64)
+        return np.concatenate(parts_b), np.concatenate(parts_o)
+
+    def slot_mapping(self, slots: Sequence[int], starts: Sequence[int], counts: Sequence[int]) -> torch.Tensor:
+        """Flat int64 slots ``block * block_size + offset`` for the same tokens as :meth:`write_index`."""
+        blocks, offsets = self._write_index_np(slots, starts, counts)
+        return torch.from_numpy(blocks * self.block_size + offsets).to(self.k.device)
+
+    def packed_prefill_context(self, slots: Sequence[int], lengths: Sequence[int]) -> "PackedPrefillContext":
+        return PackedPrefillContext(self, slots, lengths)
+
+    def decode_context(self, slots: Sequence[int]) -> "PagedDecodeContext":
+        return PagedDecodeContext(self, slots)
+
+
+class PagedDecodeContext:
+    """One batched decode step: B sequences, one new token each (engine/kv_cache.py:582-624).
+
+    Built once per step on the host; every layer's ``attend`` reuses its device tensors:
+
+    * ``positions`` int64 ``[B]`` (RoPE positions, where each new token goes);
+    * ``slot_mapping`` int64 ``[B]`` = ``write_blocks * block_size + write_offsets``;
+    * ``block_tables`` int32 ``[B, nb]``, rows padded with block 0 like the reference's
+      ``tables`` (``nb`` = blocks of the longest sequence);
+    * ``context_lens`` int32 ``[B]`` = ``positions + 1`` (keys each query attends).
+    """
+
+    def __init__(self, cache: PagedKVCache, slots: Sequence[int]) -> None:
+        self.cache = cache
+        self.slots = list(slots)
+        bs = cache.block_size
+        pos = np.asarray([cache.lengths[s] for s in self.slots], dtype=np.int64)
+        tables = [cache.block_tables[s] for s in self.slots]
+        if any(p // bs >= len(t) for p, t in zip(pos.tolist(), tables)):
+            raise ValueError("a sequence has no block for its next token (call ensure_capacity first)")
+        cache.prepare_writes(self.slots, pos.tolist(), [1] * len(self.slots))
+        tables = [cache.block_tables[s] for s in self.slots]  # copy-on-write may have replaced blocks
+        nb = int(pos.max()) // bs + 1 if len(pos) else 1
+        padded = np.zeros((len(self.slots), nb), dtype=np.int32)
+        for i, t in enumerate(tables):
+            row = t[:nb]
+            padded[i, :len(row)] = row
+        write_blocks = padded[np.arange(len(self.slots)), pos // bs].astype(np.int64)
+        write_offsets = pos % bs
+        dev = cache.k.device
+        i64 = torch.from_numpy(np.concatenate([pos, write_blocks, write_offsets, write_blocks * bs + write_offsets]))
+        i64 = i64.to(dev)
+        b = len(self.slots)
+        self.positions, self.write_blocks, self.write_offsets, self.slot_mapping = i64.split(b)
+        i32 = torch.from_numpy(np.concatenate([(pos + 1).astype(np.int32), padded.reshape(-1)])).to(dev)
+        self.context_lens = i32[:b]
+        self.block_tables = i32[b:].view(b, nb)
+        self.num_blocks = nb
+        self.kv_len = nb * bs
+        self.scale = 1.0 / (cache.head_dim ** 0.5)
+        self._mask: torch.Tensor | None = None
+
+    @property
+    def tables(self) -> torch.Tensor:
+        """The padded block tables (int32 here; int64 in the reference)."""
+        return self.block_tables
+
+    @property
+    def mask(self) -> torch.Tensor:
+        """``[B, 1, 1, kv_len]`` bool mask of the reference (built on demand; the kernel does not need it)."""
+        if self._mask is None:
+            keys = torch.arange(self.kv_len, device=self.positions.device)
+            self._mask = (keys <= self.positions.unsqueeze(1))[:, None, None, :]
+        return self._mask
+
+    def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
+        paged_ops.kv_append(k_layer, v_layer, k[:, :, 0], v[:, :, 0], self.slot_mapping)
+        out = paged_ops.paged_decode(q[:, :, 0], k_layer, v_layer, self.block_tables, self.context_lens,
+                                     scale=self.scale, max_blocks=self.num_blocks)
+        return out.unsqueeze(2)
+
+    def commit(self) -> None:
+        for s in self.slots:
+            self.cache.lengths[s] += 1
+
+
+class PackedPrefillContext:
+    """Several prompts packed end to end in one forward pass (engine/kv_cache.py:218-301).
+
+    The scatter of the N packed tokens into the pool is the append kernel. Attention over
+    the packed tokens (block-diagonal causal mask, plus read-back of a cached prefix when
+    some sequence already has tokens) is torch SDPA, as in the reference.
+    """
+
+    def __init__(self, cache: PagedKVCache, slots: Sequence[int], lengths: Sequence[int]) -> None:
+        self.cache = cache
+        self.slots = list(slots)
+        self.lengths = list(lengths)
+        self.starts = [cache.lengths[s] for s in self.slots]
+        for s, start, n in zip(self.slots, self.starts, self.lengths):
+            if not cache.ensure_capacity(s, start + n):
+                raise ValueError(f"no room in the KV cache for {start + n} tokens")
+        cache.prepare_writes(self.slots, self.starts, self.lengths)
+        dev = cache.k.device
+        seg = torch.repeat_interleave(torch.arange(len(self.slots), device=dev),
+                                      torch.tensor(self.lengths, device=dev))
+        self.positions = torch.from_numpy(np.concatenate(
+            [np.arange(a, a + n, dtype=np.int64) for a, n in zip(self.starts, self.lengths)])).to(dev)
+        blocks, offsets = cache._write_index_np(self.slots, self.starts, self.lengths)
+        both = torch.from_numpy(np.concatenate([blocks, offsets, blocks * cache.block_size + offsets])).to(dev)
+        n_tok = blocks.shape[0]
+        self.write_at = (both[:n_tok], both[n_tok:2 * n_tok])
+        self.slot_mapping = both[2 * n_tok:]
+        self.has_prefix = any(self.starts)
+        if self.has_prefix:
+            ends = [a + n for a, n in zip(self.starts, self.lengths)]
+            self.read_at = cache.write_index(self.slots, [0] * len(self.slots), ends)
+            key_seg = torch.repeat_interleave(torch.arange(len(self.slots), device=dev), torch.tensor(ends, device=dev))
+            key_pos = torch.cat([torch.arange(e, device=dev) for e in ends])
+            self.mask = (seg[:, None] == key_seg[None, :]) & (key_pos[None, :] <= self.positions[:, None])
+        elif len(self.slots) == 1:
+            self.mask = None
+        else:
+            idx = torch.arange(seg.shape[0], device=dev)
+            self.mask = (seg[:, None] == seg[None, :]) & (idx[None, :] <= idx[:, None])
+        self.last_index = torch.tensor(self.lengths, device=dev).cumsum(0) - 1
+
+    def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
+        # k[0] is [Hkv, N, D]; the append kernel takes [N, Hkv, D] views with any strides.
+        paged_ops.kv_append(k_layer, v_layer, k[0].transpose(0, 1), v[0].transpose(0, 1), self.slot_mapping)
+        if self.has_prefix:
+            rb, ro = self.read_at
+            keys = k_layer[rb, :, ro].transpose(0, 1).unsqueeze(0)
+            values = v_layer[rb, :, ro].transpose(0, 1).unsqueeze(0)
+            return sdpa_attention(q, keys, values, attn_mask=self.mask)
+        if self.mask is None:
+            return sdpa_attention(q, k, v, is_causal=True)
+        return sdpa_attention(q, k, v, attn_mask=self.mask)
+
+    def commit(self) -> None:
+        for slot, start, n in zip(self.slots, self.starts, self.lengths):
+            self.cache.lengths[slot] = start + n

@@ -1,0 +1,183 @@
+"""Tensor-level entry points of the paged KV-cache kernels.
+
+Each function validates shapes on the host, then passes raw device pointers, element
+strides and the current HIP stream through the C ABI (``include/mipaged.h``). Nothing
+here computes on the CPU: tensors that are not on a ROCm device raise.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _native
+
+_DTYPE_CODES = {torch.float32: _native.MIP_F32, torch.float16: _native.MIP_F16, torch.bfloat16: _native.MIP_BF16}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported KV dtype {dtype}; expected float32, float16 or bfloat16") from None
+
+
+def _require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(
+                "the paged KV-cache kernels run only on a ROCm GPU device (got a tensor on "
+                f"{t.device}); there is no CPU path"
+            )
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+              slot_mapping: torch.Tensor) -> None:
+    """Write token i's K/V rows (``k[i, h, :]``) to pool slot ``slot_mapping[i]``.
+
+    ``k_cache``/``v_cache``: one layer of the pool, ``[num_blocks + 1, Hkv, block_size, D]``
+    contiguous. ``k``/``v``: ``[N, Hkv, D]`` with any token/head strides and a contiguous
+    last dimension. ``slot_mapping``: int64 ``[N]``, ``block * block_size + offset``.
+    Follows engine/kv_cache.py:613-614 and :286-289 (bit-exact data movement).
+    """
+    _require_device(k_cache, v_cache, k, v, slot_mapping)
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache must be contiguous [num_blocks, Hkv, block_size, D] tensors of one shape")
+    nb, hkv, bs, d = k_cache.shape
+    if k.dim() != 3 or k.shape != v.shape or k.shape[1:] != (hkv, d):
+        raise ValueError(f"k/v must be [N, {hkv}, {d}], got {tuple(k.shape)} and {tuple(v.shape)}")
+    if k.dtype != k_cache.dtype or v.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
+        raise TypeError("k, v and the cache must share one dtype")
+    if k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("the last (head_dim) dimension of k/v must be contiguous")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or slot_mapping.shape[0] != k.shape[0]:
+        raise ValueError("slot_mapping must be int64 [N]")
+    if not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be contiguous")
+    n = k.shape[0]
+    if n == 0:
+        return
+    lib = _native.load()
+    st = lib.mip_kv_append(
+        k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), nb, slot_mapping.data_ptr(), n, hkv, d, bs,
+        dtype_code(k_cache.dtype), _stream_ptr(k_cache.device),
+    )
+    _native.check(st, "mip_kv_append")
+
+
+class _Workspace:
+    """One zero-initialised scratch buffer per device, grown on demand.
+
+    The decode kernel leaves its counters at zero when it finishes, so the buffer is
+    zero-filled only when it is (re)allocated. Calls that use it must be ordered (one
+    stream, or graph replays on that stream): two decode calls running concurrently on
+    different streams of one device would race on it; pass ``workspace=`` to each instead.
+    Allocate it before graph capture (one eager call with the largest shape).
+    """
+
+    def __init__(self) -> None:
+        self._bufs: dict[int, torch.Tensor] = {}
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        key = device.index if device.index is not None else torch.cuda.current_device()
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+_workspace = _Workspace()
+
+
+def decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+                           max_blocks: int, dtype: torch.dtype) -> int:
+    return int(_native.load().mip_paged_decode_workspace(batch, num_heads, num_kv_heads, head_dim, block_size,
+                                                         max_blocks, dtype_code(dtype)))
+
+
+def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                 context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
+                 max_blocks: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention over paged K/V for one query token per sequence.
+
+    ``q``: ``[B, Hq, D]`` (last dim contiguous). ``k_cache``/``v_cache``: one layer,
+    ``[num_blocks + 1, Hkv, block_size, D]``. ``block_tables``: int32 ``[B, >= max_blocks]``.
+    ``context_lens``: int32 ``[B]`` (keys attended = positions + 1). Returns ``out``
+    ``[B, Hq, D]`` in q's dtype. Follows engine/kv_cache.py:615-620 and
+    engine/model.py:126-147 with ``scale = 1/sqrt(D)`` by default.
+    """
+    _require_device(q, k_cache, v_cache, block_tables, context_lens)
+    if q.dim() != 3 or q.stride(2) != 1:
+        raise ValueError("q must be [B, Hq, D] with a contiguous last dimension")
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache must be contiguous [num_blocks, Hkv, block_size, D] tensors of one shape")
+    nb, hkv, bs, d = k_cache.shape
+    b, hq, dq = q.shape
+    if dq != d or hq % hkv != 0:
+        raise ValueError(f"q {tuple(q.shape)} does not match the cache (Hkv={hkv}, D={d})")
+    if q.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
+        raise TypeError("q and the cache must share one dtype")
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != b:
+        raise ValueError("block_tables must be int32 [B, max_blocks]")
+    if block_tables.stride(1) != 1:
+        raise ValueError("block_tables rows must be contiguous")
+    if context_lens.dtype != torch.int32 or context_lens.shape != (b,) or not context_lens.is_contiguous():
+        raise ValueError("context_lens must be contiguous int32 [B]")
+    mb = block_tables.shape[1] if max_blocks is None else int(max_blocks)
+    if mb < 1 or mb > block_tables.shape[1]:
+        raise ValueError(f"max_blocks={mb} is outside [1, {block_tables.shape[1]}]")
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
+    elif out.shape != (b, hq, d) or out.dtype != q.dtype or out.stride(2) != 1:
+        raise ValueError("out must be [B, Hq, D] in q's dtype with a contiguous last dimension")
+    if b == 0:
+        return out
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    code = dtype_code(q.dtype)
+    lib = _native.load()
+    need = int(lib.mip_paged_decode_workspace(b, hq, hkv, d, bs, mb, code))
+    if workspace is None:
+        workspace = _workspace.get(q.device, need)
+    elif need and workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, needs {need}")
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    st = lib.mip_paged_decode(
+        out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), nb, block_tables.data_ptr(), block_tables.stride(0),
+        context_lens.data_ptr(), b, hq, hkv, d, bs, mb, scale, ws_ptr, ws_bytes, code, _stream_ptr(q.device),
+    )
+    _native.check(st, "mip_paged_decode")
+    return out
+
+
+def copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs: torch.Tensor) -> None:
+    """Copy whole blocks, every layer, K and V: ``pool[:, dst] = pool[:, src]`` per (src, dst) row.
+
+    ``k_pool``/``v_pool``: ``[num_layers, num_blocks + 1, Hkv, block_size, D]`` contiguous.
+    ``pairs``: int64 ``[n, 2]`` on the pool's device. Bitwise copy (no reference
+    counterpart; used for copy-on-write of shared prefix blocks).
+    """
+    _require_device(k_pool, v_pool, pairs)
+    if k_pool.shape != v_pool.shape or k_pool.dim() != 5 or not (k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise ValueError("k_pool/v_pool must be contiguous [L, num_blocks, Hkv, block_size, D] tensors of one shape")
+    if pairs.dtype != torch.int64 or pairs.dim() != 2 or pairs.shape[1] != 2 or not pairs.is_contiguous():
+        raise ValueError("pairs must be contiguous int64 [n, 2]")
+    n = pairs.shape[0]
+    if n == 0:
+        return
+    num_layers, nb = k_pool.shape[0], k_pool.shape[1]
+    block_bytes = k_pool[0, 0].numel() * k_pool.element_size()
+    st = _native.load().mip_copy_blocks(k_pool.data_ptr(), v_pool.data_ptr(), pairs.data_ptr(), n, num_layers, nb,
+                                        block_bytes, _stream_ptr(k_pool.device))
+    _native.check(st, "mip_copy_blocks")

@@ -1,0 +1,360 @@
+"""GPU parity of the three HIP kernels against the CPU oracle, through the C ABI.
+
+Bar: KV append and block copy bit-exact (every byte of the pool, touched or not);
+paged decode attention within 2e-3 max-abs of the float64 oracle for fp16/bf16 (the
+fp32-accumulate bound), 2e-5 for fp32.
+"""
+
+from __future__ import annotations
+
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import paged_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+TOL = {"float32": 2e-5, "float16": 2e-3, "bfloat16": 2e-3}
+
+
+def storage(t: torch.Tensor) -> np.ndarray:
+    """CPU numpy view of a tensor's storage: float32 values, or uint16 bits for 16-bit dtypes."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.float32:
+        return t.numpy().copy()
+    return t.view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def values(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def dname(dtype: torch.dtype) -> str:
+    return {v: k for k, v in DTYPES.items()}[dtype]
+
+
+MANTISSA_BITS = {"float32": 23, "float16": 10, "bfloat16": 7}
+
+
+def half_ulp(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Half the spacing of ``dtype`` at |x|: the error of rounding an exact result once to the output dtype."""
+    ax = np.maximum(np.abs(x), np.finfo(np.float32).tiny)
+    return 0.5 * np.exp2(np.floor(np.log2(ax)) - MANTISSA_BITS[dtype])
+
+
+def attention_error(got: np.ndarray, want: np.ndarray, dtype: str) -> float:
+    """Max error beyond the output's own final rounding (the fp32-accumulate error, bounded by TOL)."""
+    return float((np.abs(got - want) - half_ulp(want, dtype)).max())
+
+
+# ----------------------------------------------------------------------------- append
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+def test_append_decode_bit_exact(gpu, dtype):
+    from engine import paged_ops
+
+    announce(f"append decode {dtype}")
+    dt = DTYPES[dtype]
+    g = torch.Generator().manual_seed(1)
+    nb, hkv, bs, d, batch = 64, 2, 16, 64, 40
+    k_cache = torch.randn(nb + 1, hkv, bs, d, generator=g).to(dt).to(gpu)
+    v_cache = torch.randn(nb + 1, hkv, bs, d, generator=g).to(dt).to(gpu)
+    slots = torch.tensor(random.Random(2).sample(range((nb + 1) * bs), batch), dtype=torch.int64)
+    # k as a contiguous [B, Hkv, D]; v as a strided view out of a wider row (like the qkv split).
+    k_new = torch.randn(batch, hkv, d, generator=g).to(dt)
+    wide = torch.randn(batch, 3 * hkv * d, generator=g).to(dt)
+    v_new = wide[:, 2 * hkv * d:].view(batch, hkv, d)
+    kc, vc = storage(k_cache), storage(v_cache)
+    ref.append(kc, vc, (slots // bs).numpy(), (slots % bs).numpy(), storage(k_new), storage(v_new))
+    paged_ops.kv_append(k_cache, v_cache, k_new.to(gpu), wide.to(gpu)[:, 2 * hkv * d:].view(batch, hkv, d),
+                        slots.to(gpu))
+    torch.cuda.synchronize()
+    assert np.array_equal(storage(k_cache), kc)
+    assert np.array_equal(storage(v_cache), vc)
+
+
+def test_append_packed_prefill_views(gpu):
+    """The packed-prefill scatter: k[0].transpose(0, 1) and a v view of the fused qkv output."""
+    from engine import paged_ops
+
+    announce("append packed fp16")
+    dt = torch.float16
+    g = torch.Generator().manual_seed(3)
+    nb, hkv, bs, d, n, hq = 300, 2, 16, 64, 3000, 14
+    width = (hq + 2 * hkv) * d
+    k_cache = torch.zeros(nb + 1, hkv, bs, d, dtype=dt, device=gpu)
+    v_cache = torch.zeros_like(k_cache)
+    qkv = torch.randn(1, n, width, generator=g).to(dt)
+    k = qkv[..., hq * d:(hq + hkv) * d].reshape(1, n, hkv, d).transpose(1, 2).contiguous()  # post-RoPE k is contiguous
+    v = qkv[..., (hq + hkv) * d:].view(1, n, hkv, d).transpose(1, 2)                         # v stays a view
+    perm = list(range(nb))
+    random.Random(4).shuffle(perm)
+    blocks = np.asarray([perm[i // bs] for i in range(n)], dtype=np.int64)
+    offsets = np.arange(n, dtype=np.int64) % bs
+    slots = torch.from_numpy(blocks * bs + offsets)
+    kc, vc = storage(k_cache), storage(v_cache)
+    ref.append(kc, vc, blocks, offsets, storage(k[0].transpose(0, 1)), storage(v[0].transpose(0, 1)))
+    kg, qkvg = k.to(gpu), qkv.to(gpu)
+    vg = qkvg[..., (hq + hkv) * d:].view(1, n, hkv, d).transpose(1, 2)
+    paged_ops.kv_append(k_cache, v_cache, kg[0].transpose(0, 1), vg[0].transpose(0, 1), slots.to(gpu))
+    torch.cuda.synchronize()
+    assert np.array_equal(storage(k_cache), kc)
+    assert np.array_equal(storage(v_cache), vc)
+
+
+@pytest.mark.parametrize("dtype,d", [("bfloat16", 4), ("float16", 6), ("float32", 3), ("float32", 128)])
+def test_append_narrow_rows_and_skipped_slots(gpu, dtype, d):
+    from engine import paged_ops
+
+    announce(f"append narrow {dtype} d={d}")
+    dt = DTYPES[dtype]
+    g = torch.Generator().manual_seed(5)
+    nb, hkv, bs = 10, 3, 4
+    k_cache = torch.randn(nb + 1, hkv, bs, d, generator=g).to(dt).to(gpu)
+    v_cache = torch.randn(nb + 1, hkv, bs, d, generator=g).to(dt).to(gpu)
+    slots = torch.tensor([5, -1, 43, (nb + 1) * bs, 0, 17, 10 ** 9], dtype=torch.int64)
+    k_new = torch.randn(len(slots), hkv, d, generator=g).to(dt)
+    v_new = torch.randn(len(slots), hkv, d, generator=g).to(dt)
+    kc, vc = storage(k_cache), storage(v_cache)
+    keep = [(i, int(s)) for i, s in enumerate(slots) if 0 <= s < (nb + 1) * bs]
+    idx = np.asarray([i for i, _ in keep])
+    sl = np.asarray([s for _, s in keep])
+    ref.append(kc, vc, sl // bs, sl % bs, storage(k_new)[idx], storage(v_new)[idx])
+    paged_ops.kv_append(k_cache, v_cache, k_new.to(gpu), v_new.to(gpu), slots.to(gpu))
+    torch.cuda.synchronize()
+    assert np.array_equal(storage(k_cache), kc)
+    assert np.array_equal(storage(v_cache), vc)
+
+
+# ----------------------------------------------------------------------------- block copy
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_copy_blocks_bit_exact(gpu, dtype):
+    from engine import paged_ops
+
+    announce(f"copy_blocks {dtype}")
+    dt = DTYPES[dtype]
+    g = torch.Generator().manual_seed(6)
+    layers, nb, hkv, bs, d = 3, 40, 2, 16, 64
+    k = torch.randn(layers, nb + 1, hkv, bs, d, generator=g).to(dt).to(gpu)
+    v = torch.randn(layers, nb + 1, hkv, bs, d, generator=g).to(dt).to(gpu)
+    rng = random.Random(7)
+    ids = rng.sample(range(nb + 1), 24)
+    pairs = [(ids[i], ids[i + 12]) for i in range(12)] + [(3, -1), (nb + 5, 4)]  # last two are skipped
+    kc, vc = storage(k), storage(v)
+    ref.copy_blocks(kc, vc, pairs[:12])
+    paged_ops.copy_blocks(k, v, torch.tensor(pairs, dtype=torch.int64, device=gpu))
+    torch.cuda.synchronize()
+    assert np.array_equal(storage(k), kc)
+    assert np.array_equal(storage(v), vc)
+
+
+# ----------------------------------------------------------------------------- paged decode attention
+
+
+def _random_case(dtype, batch, hq, hkv, d, bs, lens, nb_extra=3, seed=0, stale=None):
+    """Pool with scattered tables; returns device tensors and the CPU float pools for the oracle."""
+    dt = DTYPES[dtype]
+    g = torch.Generator().manual_seed(seed)
+    need = [math.ceil(n / bs) for n in lens]
+    nb = sum(need) + nb_extra
+    perm = list(range(nb))
+    random.Random(seed + 1).shuffle(perm)
+    tables, cur = [], 0
+    for n in need:
+        tables.append(perm[cur:cur + n])
+        cur += n
+    width = max(max(need), 1)
+    bt = np.zeros((batch, width + 2), dtype=np.int32)  # extra columns never read
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = t
+    k_pool = torch.randn(nb + 1, hkv, bs, d, generator=g).to(dt)
+    v_pool = torch.randn(nb + 1, hkv, bs, d, generator=g).to(dt)
+    if stale is not None:
+        # Poison every row that no query may read: padding, tails of last blocks, free blocks.
+        live = np.zeros((nb + 1, bs), dtype=bool)
+        for t, n in zip(tables, lens):
+            for j in range(n):
+                live[t[j // bs], j % bs] = True
+        dead = torch.from_numpy(~live)
+        k_pool[dead.nonzero(as_tuple=True)[0], :, dead.nonzero(as_tuple=True)[1]] = stale
+        v_pool[dead.nonzero(as_tuple=True)[0], :, dead.nonzero(as_tuple=True)[1]] = stale
+    q = torch.randn(batch, hq, d, generator=g).to(dt)
+    return q, k_pool, v_pool, tables, bt, width
+
+
+def _check_decode(gpu, dtype, batch, hq, hkv, d, bs, lens, seed=0, stale=None, max_blocks=None):
+    from engine import paged_ops
+
+    q, k_pool, v_pool, tables, bt, width = _random_case(dtype, batch, hq, hkv, d, bs, lens, seed=seed, stale=stale)
+    mb = width if max_blocks is None else max_blocks
+    out = paged_ops.paged_decode(q.to(gpu), k_pool.to(gpu), v_pool.to(gpu), torch.from_numpy(bt).to(gpu),
+                                 torch.tensor(lens, dtype=torch.int32, device=gpu), max_blocks=mb)
+    torch.cuda.synchronize()
+    want = ref.attention_f64(values(q), values(k_pool), values(v_pool), tables, lens, bs)
+    got = values(out)
+    assert np.isfinite(got).all()
+    err = attention_error(got, want, dtype)
+    assert err <= TOL[dtype], f"error beyond output rounding {err:.3g} > {TOL[dtype]}"
+    return err
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("d,hq,hkv,bs", [(64, 14, 2, 16), (128, 28, 4, 32), (8, 4, 2, 4), (64, 8, 8, 16),
+                                         (32, 6, 2, 8), (256, 8, 1, 16), (16, 5, 1, 2)])
+def test_paged_decode_shapes(gpu, dtype, d, hq, hkv, bs):
+    announce(f"paged_decode {dtype} d={d} hq={hq} hkv={hkv} bs={bs}")
+    lens = [1, bs - 1 if bs > 1 else 1, bs, bs + 1, 37, 511, 512, 513, 1200, 2049]
+    _check_decode(gpu, dtype, len(lens), hq, hkv, d, bs, lens, seed=d + hq)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_paged_decode_never_reads_stale_rows(gpu, dtype):
+    """NaN in every row a query may not see (padding, last-block tails, free blocks) must not leak."""
+    announce(f"paged_decode stale NaN {dtype}")
+    lens = [3, 16, 17, 100, 700, 1500]
+    _check_decode(gpu, dtype, len(lens), 14, 2, 64, 16, lens, seed=11, stale=float("nan"))
+
+
+def test_paged_decode_large_logits_rescale(gpu):
+    """Scores spanning hundreds of units exercise the lazy running-max rescale."""
+    from engine import paged_ops
+
+    announce("paged_decode large logits")
+    lens = [50, 600, 1800]
+    q, k_pool, v_pool, tables, bt, width = _random_case("float32", 3, 14, 2, 64, 16, lens, seed=12)
+    q = q * 40.0
+    ramp = torch.linspace(-3, 3, k_pool.shape[0]).view(-1, 1, 1, 1)
+    k_pool = k_pool * ramp
+    out = paged_ops.paged_decode(q.to(gpu), k_pool.to(gpu), v_pool.to(gpu), torch.from_numpy(bt).to(gpu),
+                                 torch.tensor(lens, dtype=torch.int32, device=gpu))
+    torch.cuda.synchronize()
+    want = ref.attention_f64(values(q), values(k_pool), values(v_pool), tables, lens, 16)
+    assert np.abs(values(out) - want).max() < 1e-4
+
+
+def test_paged_decode_config1_golden(gpu):
+    """Config 1 (fp32, B=8, 14q/2kv, D=64, pool 512x16): append then attention, vs the reference path."""
+    from engine import workloads
+
+    announce("config1 decode step fp32")
+    batch = workloads.build_decode_batch(workloads.SHAPES[1], gpu, seed=0)
+    cache = batch.cache
+    q, k, v = workloads.step_inputs(batch, seed=0)
+    k_cpu, v_cpu = cache.k[0].cpu().clone(), cache.v[0].cpu().clone()
+    tables = [list(cache.block_tables[s]) for s in batch.slots]
+    inputs = ref.decode_inputs(batch.ctx, tables, cache.block_size)
+    want_t = ref.paged_decode_torch(q.cpu(), k_cpu, v_cpu, k.cpu(), v.cpu(), inputs)
+    ctx = cache.decode_context(batch.slots)
+    got = ctx.attend(0, q, k, v)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.k[0].cpu(), k_cpu) and torch.equal(cache.v[0].cpu(), v_cpu)  # append bit-exact
+    want64 = ref.attention_f64(values(q[:, :, 0]), k_cpu.numpy(), v_cpu.numpy(), tables, inputs["context_lens"], 16)
+    assert np.abs(values(got[:, :, 0]) - want64).max() < 2e-5
+    assert np.abs(values(got) - want_t.numpy()).max() < 2e-5
+
+
+@pytest.mark.parametrize("cfg", [2, 3])
+def test_decode_step_full_size(gpu, cfg):
+    """Configs 2 (fp16 B=32) and 3 (bf16 B=256, churned pool): one layer's append + attention vs float64."""
+    from engine import workloads
+
+    announce(f"config{cfg} decode step")
+    shape = workloads.SHAPES[cfg]
+    small = workloads.DecodeShape(**{**shape.__dict__, "num_layers": 1})
+    batch = workloads.build_decode_batch(small, gpu, seed=0)
+    cache = batch.cache
+    q, k, v = workloads.step_inputs(batch, seed=1)
+    ctx = cache.decode_context(batch.slots)
+    out = ctx.attend(0, q, k, v)
+    torch.cuda.synchronize()
+    tables = [list(cache.block_tables[s]) for s in batch.slots]
+    kp, vp = values(cache.k[0]), values(cache.v[0])
+    lens = [n + 1 for n in batch.ctx]
+    # the append wrote the new rows where the reference index math says
+    inputs = ref.decode_inputs(batch.ctx, tables, cache.block_size)
+    assert np.array_equal(kp[inputs["write_blocks"], :, inputs["write_offsets"]], values(k[:, :, 0]))
+    assert np.array_equal(vp[inputs["write_blocks"], :, inputs["write_offsets"]], values(v[:, :, 0]))
+    want = ref.attention_f64(values(q[:, :, 0]), kp, vp, tables, lens, cache.block_size)
+    got = values(out[:, :, 0])
+    err = np.abs(got - want).max()
+    print(f"config{cfg} max-abs err {err:.3g}, max |out| {np.abs(want).max():.3g}")
+    assert err <= 2e-3  # plain max-abs: at these context lengths |out| < 0.5, so rounding fits too
+    assert attention_error(got, want, dname(shape.dtype)) <= 2e-3
+
+
+def test_decode_context_matches_per_sequence_sdpa(gpu):
+    """Reference tests/test_kv_cache.py:179-207 restated on the GPU path."""
+    from engine.kv_cache import PagedKVCache
+
+    announce("decode context vs per-sequence sdpa")
+    torch.manual_seed(0)
+    cache = PagedKVCache(num_layers=1, num_kv_heads=2, head_dim=8, num_blocks=12, block_size=4, max_seqs=4,
+                         max_len=32, dtype=torch.float32, device=gpu)
+    heads, kv_heads, dim = 4, 2, 8
+    lengths = [6, 9, 3]
+    slots = [cache.allocate(0) for _ in lengths]
+    for n_blocks in range(1, 4):
+        for s, n in zip(slots, lengths):
+            cache.ensure_capacity(s, min(n + 1, n_blocks * 4))
+    keys_by_seq = []
+    for s, n in zip(slots, lengths):
+        k = torch.randn(1, kv_heads, n, dim, device=gpu)
+        v = torch.randn(1, kv_heads, n, dim, device=gpu)
+        ctx = cache.packed_prefill_context([s], [n])
+        ctx.attend(0, torch.randn(1, heads, n, dim, device=gpu), k, v)
+        ctx.commit()
+        keys_by_seq.append((k, v))
+    assert cache.block_tables[slots[0]] != list(range(cache.block_tables[slots[0]][0],
+                                                      cache.block_tables[slots[0]][0] + 2))
+    q = torch.randn(3, heads, 1, dim, device=gpu)
+    k_new, v_new = torch.randn(3, kv_heads, 1, dim, device=gpu), torch.randn(3, kv_heads, 1, dim, device=gpu)
+    ctx = cache.decode_context(slots)
+    out = ctx.attend(0, q, k_new, v_new)
+    for b, (k, v) in enumerate(keys_by_seq):
+        full_k = torch.cat([k, k_new[b:b + 1]], dim=2).cpu()
+        full_v = torch.cat([v, v_new[b:b + 1]], dim=2).cpu()
+        want = ref.sdpa_attention(q[b:b + 1].cpu(), full_k, full_v)
+        torch.testing.assert_close(out[b:b + 1].cpu(), want, rtol=1e-5, atol=1e-6)
+    ctx.commit()
+    assert [cache.lengths[s] for s in slots] == [7, 10, 4]
+
+
+def test_paged_decode_graph_replay(gpu):
+    """Append + attention captured in a HIP graph: every replay equals the eager result."""
+    from engine import paged_ops
+
+    announce("graph capture append+decode")
+    lens = [40, 700, 1300, 5]
+    q, k_pool, v_pool, tables, bt, width = _random_case("bfloat16", 4, 14, 2, 64, 16, lens, seed=21)
+    qg, kg, vg = q.to(gpu), k_pool.to(gpu), v_pool.to(gpu)
+    btg = torch.from_numpy(bt).to(gpu)
+    cl = torch.tensor(lens, dtype=torch.int32, device=gpu)
+    slots = torch.tensor([tables[i][(n - 1) // 16] * 16 + (n - 1) % 16 for i, n in enumerate(lens)],
+                         dtype=torch.int64, device=gpu)
+    k_new = torch.randn(4, 2, 64, device=gpu).to(torch.bfloat16)
+    v_new = torch.randn(4, 2, 64, device=gpu).to(torch.bfloat16)
+    out = torch.empty_like(qg)
+    eager = paged_ops.paged_decode(qg, kg, vg, btg, cl)  # also allocates the workspace outside capture
+    paged_ops.kv_append(kg, vg, k_new, v_new, slots)
+    eager = paged_ops.paged_decode(qg, kg, vg, btg, cl).clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_ops.kv_append(kg, vg, k_new, v_new, slots)
+        paged_ops.paged_decode(qg, kg, vg, btg, cl, out=out)
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs"
+        _ = (qg.float() * 2).sum().item()  # unrelated eager work between replays
