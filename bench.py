@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged KV-cache decode path on one MI355X.
+
+Workload (the metric's configuration): Qwen2.5-0.5B attention shape (14 query / 2 KV heads,
+head_dim 64), bf16, batch 256, contexts log-uniform in [128, 4096], block size 16, the pool
+fragmented by a seeded 5,000-event alloc/free churn trace, 24 layers. One step = for each
+of the 24 layers: KV append of the step's 256 new tokens + paged decode attention. Inputs
+are resident in HBM before the timed region; the pool holds N(0, 1) data.
+
+Reported (one JSON line on stdout):
+  value         algorithmic bytes of the step (append + attention, 24 layers) / step time, GB/s
+  roofline      the paged decode-attention kernel alone: algorithmic bytes per launch /
+                average launch duration (HIP events over a timed loop of its launches),
+                against the 8 TB/s HBM peak; traffic = measured HBM bytes per launch when a
+                counter summary exists under profiles/
+  decode_tok_s  B / full decode-step time of a random-init Qwen2.5-0.5B (embedding, 24 layers
+                with GEMMs, RoPE, append, attention, MLP, final norm, logits)
+  cpu_baseline  the reference's torch CPU path (index_put_ append + table gather + SDPA,
+                the oracle's restatement) timed on this host's cores for one layer, fp32
+
+Algorithmic bytes per layer (e = element bytes, L_b = context + 1):
+  attention = sum_b 2*Hkv*L_b*D*e  +  2*B*Hq*D*e (q, out)  +  sum_b ceil(L_b/BS)*4 (table)  +  4*B (lens)
+  append    = 2 * (2*B*Hkv*D*e)  +  8*B (slot mapping)
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "mini-inference_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "paged decode-attn HBM GB/s (% of peak) + decode tok/s, Qwen2.5-0.5B b256"
+TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_bf16_b256_ctx128-4096_traffic.json"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def attention_bytes(lens: list[int], shape) -> int:
+    e = shape.dtype.itemsize
+    kv = sum(2 * shape.num_kv_heads * n * shape.head_dim * e for n in lens)
+    qo = 2 * shape.batch * shape.num_heads * shape.head_dim * e
+    tables = sum(-(-n // shape.block_size) * 4 for n in lens)
+    return kv + qo + tables + 4 * shape.batch
+
+
+def append_bytes(shape) -> int:
+    e = shape.dtype.itemsize
+    return 2 * (2 * shape.batch * shape.num_kv_heads * shape.head_dim * e) + 8 * shape.batch
+
+
+def time_loop(fn, iters: int) -> float:
+    """Seconds per iteration of ``fn`` on the current stream, by HIP events around ``iters`` calls."""
+    import torch
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / iters
+
+
+def cpu_baseline(batch, layer_q, layer_k, layer_v, budget_s: float) -> dict:
+    """The reference CPU torch path (oracle restatement) on one layer, fp32, this host's cores."""
+    import torch
+
+    from oracle import paged_ref as ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cache = batch.cache
+    tables = [list(cache.block_tables[s]) for s in batch.slots]
+    inputs = ref.decode_inputs(batch.ctx, tables, cache.block_size)
+    # Only the blocks the batch owns matter to the per-step work; copy those into a compact fp32 pool.
+    used = sorted({b for t in tables for b in t})
+    remap = {b: i for i, b in enumerate(used)}
+    idx = torch.tensor(used, device=cache.k.device)
+    k_cpu = cache.k[0].index_select(0, idx).float().cpu()
+    v_cpu = cache.v[0].index_select(0, idx).float().cpu()
+    compact = [[remap[b] for b in t] for t in tables]
+    inputs = ref.decode_inputs(batch.ctx, compact, cache.block_size)
+    q, k, v = layer_q.float().cpu(), layer_k.float().cpu(), layer_v.float().cpu()
+    times = []
+    t_start = time.perf_counter()
+    warm = 2
+    while True:
+        t0 = time.perf_counter()
+        ref.paged_decode_torch(q, k_cpu, v_cpu, k, v, inputs)
+        times.append(time.perf_counter() - t0)
+        runs = len(times) - warm
+        if runs >= 5 or (runs >= 1 and time.perf_counter() - t_start > budget_s):
+            break
+    timed = times[warm:] if len(times) > warm else times
+    per_layer = statistics.median(timed)
+    try:
+        model = next(line.split(":", 1)[1].strip() for line in open("/proc/cpuinfo") if line.startswith("model name"))
+    except (OSError, StopIteration):
+        model = "unknown"
+    return {"per_layer_s": per_layer, "runs": len(timed), "warmup": min(warm, len(times)), "cores": cores,
+            "cpu_model": model}
+
+
+def decode_tok_s(batch, steps: int, warmup: int) -> dict:
+    """Full random-init Qwen2.5-0.5B decode step at this batch, eager, through the cache contexts."""
+    import torch
+
+    from engine.model import Qwen2Config, Qwen2ForCausalLM, random_init_
+
+    cfg = Qwen2Config.qwen2_5_0_5b()
+    dev = batch.cache.k.device
+    with torch.device(dev):
+        model = Qwen2ForCausalLM(cfg)
+    model = random_init_(model.to(dev, batch.shape.dtype), seed=0)
+    ids = torch.randint(0, cfg.vocab_size, (len(batch.slots), 1), device=dev,
+                        generator=torch.Generator(device=dev).manual_seed(5))
+
+    @torch.inference_mode()
+    def step():
+        ctx = batch.cache.decode_context(batch.slots)  # host tables + H2D, as the runner does each step
+        hidden = model(ids, ctx.positions.unsqueeze(1), ctx)
+        return model.compute_logits(hidden[:, -1]).float()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"tok_s": len(batch.slots) / t, "ms_per_step": t * 1e3, "steps": steps}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (about)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-model", action="store_true", help="skip the full-model decode tok/s measurement")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: the paged decode path runs on a single GPU here "
+              "(--gpus 1); multi-GPU runs are not part of this build.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from engine import paged_ops, workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    shape = workloads.SHAPES[3]
+    t0 = time.perf_counter()
+    batch = workloads.build_decode_batch(shape, dev, seed=0)
+    cache = batch.cache
+    log(f"workload ready in {time.perf_counter() - t0:.1f}s: B={shape.batch} layers={shape.num_layers} "
+        f"pool={cache.num_blocks} blocks, mean ctx {statistics.mean(batch.ctx):.0f}")
+
+    # Per-layer step inputs (distinct per layer) and one decode context for the step.
+    layers = shape.num_layers
+    qs, ks, vs = [], [], []
+    for layer in range(layers):
+        q, k, v = workloads.step_inputs(batch, seed=100 + layer)
+        qs.append(q)
+        ks.append(k)
+        vs.append(v)
+    ctx = cache.decode_context(batch.slots)
+    outs = [torch.empty(shape.batch, shape.num_heads, shape.head_dim, dtype=shape.dtype, device=dev)
+            for _ in range(layers)]
+    appends = [paged_ops.prepare_kv_append(cache.k[i], cache.v[i], ks[i][:, :, 0], vs[i][:, :, 0], ctx.slot_mapping)
+               for i in range(layers)]
+    decodes = [paged_ops.prepare_paged_decode(qs[i][:, :, 0], cache.k[i], cache.v[i], ctx.block_tables,
+                                              ctx.context_lens, ctx.scale, out=outs[i], max_blocks=ctx.num_blocks)[0]
+               for i in range(layers)]
+
+    def hot_step():
+        for i in range(layers):
+            appends[i]()
+            decodes[i]()
+
+    def attention_only():
+        for i in range(layers):
+            decodes[i]()
+
+    for _ in range(args.warmup):
+        hot_step()
+    torch.cuda.synchronize()
+    step_s = time_loop(hot_step, args.steps)
+    attn_s = time_loop(attention_only, args.steps) / layers
+    lens = [n + 1 for n in batch.ctx]
+    a_bytes = attention_bytes(lens, shape)
+    p_bytes = append_bytes(shape)
+    value = (a_bytes + p_bytes) * layers / step_s / 1e9
+    achieved = a_bytes / attn_s / 1e9
+    log(f"step {step_s * 1e3:.3f} ms ({value:.0f} GB/s); attention launch {attn_s * 1e6:.2f} us "
+        f"({achieved:.0f} GB/s, {achieved / HBM_PEAK_GBPS:.1%} of peak)")
+
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        try:
+            traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,1) K/V pool and q/k/v, seeded; churned block tables",
+        "config": {
+            "workload": "paged decode step (KV append + paged attention) x 24 layers, Qwen2.5-0.5B attention "
+                        "shape 14q/2kv heads d64, bf16, B=256, ctx log-uniform[128,4096], block 16, pool of "
+                        f"{cache.num_blocks} blocks fragmented by 5000 alloc/free events",
+            "batch": shape.batch,
+            "layers": layers,
+            "mean_ctx": round(statistics.mean(batch.ctx), 1),
+            "attn_bytes_per_layer": a_bytes,
+            "append_bytes_per_layer": p_bytes,
+        },
+        "frac_of_peak": round(value / HBM_PEAK_GBPS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_decode_valu<bf16, D=64, G=7>",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "avg_launch_us": round(attn_s * 1e6, 3),
+        },
+    }
+
+    if not args.no_model:
+        try:
+            dm = decode_tok_s(batch, steps=max(10, min(args.steps, 30)), warmup=3)
+            result["decode_tok_s"] = round(dm["tok_s"], 1)
+            result["decode_ms_per_step"] = round(dm["ms_per_step"], 3)
+            log(f"full-model decode: {dm['ms_per_step']:.2f} ms/step, {dm['tok_s']:.0f} tok/s")
+        except Exception as exc:  # the headline kernel numbers stand on their own
+            log(f"full-model decode failed: {exc!r}")
+            result["decode_tok_s"] = None
+
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(batch, qs[0], ks[0], vs[0], args.cpu_budget)
+        cpu_gbps = (a_bytes + p_bytes) / cb["per_layer_s"] / 1e9
+        result["cpu_baseline"] = {
+            "value": round(cpu_gbps, 3),
+            "unit": "GB/s",
+            "cores": cb["cores"],
+            "kind": "port",
+            "sample": f"reference torch CPU path (index_put_ append + table gather + SDPA), fp32, one layer of the "
+                      f"same B=256 workload, median of {cb['runs']} after {cb['warmup']} warm-ups: "
+                      f"{cb['per_layer_s'] * 1e3:.1f} ms/layer ({cb['per_layer_s'] * layers * 1e3:.0f} ms per "
+                      f"24-layer step); {cb['cpu_model']}",
+        }
+        log(f"cpu baseline: {cb['per_layer_s'] * 1e3:.1f} ms/layer on {cb['cores']} cores ({cpu_gbps:.2f} GB/s)")
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -6,25 +6,30 @@
 // softmax(q.k * scale) @ v with scale = 1/sqrt(head_dim)).
 //
 // Design
-//   * Grid = (partitions, kv heads, batch). A workgroup of kNW wavefronts owns one
-//     (sequence, kv head, partition of part_tokens keys) and computes all G query heads of
-//     that kv head, so each K/V row is read from HBM once for the whole GQA group.
-//     Workgroups whose partition starts past the sequence's context exit at once; the grid
-//     therefore depends only on max_blocks_per_seq (graph-capturable).
-//   * Within a workgroup the wavefronts take turns on "passes" of RPP consecutive keys.
+//   * Two launches. The partition kernel's grid is (partitions, kv heads, batch): a
+//     workgroup of kNW wavefronts owns one (sequence, kv head, partition of part_tokens
+//     keys) and computes all G query heads of that kv head, so each K/V row is read from HBM
+//     once for the whole GQA group. Workgroups whose partition starts past the sequence's
+//     context exit at once, so the grid depends only on max_blocks_per_seq
+//     (graph-capturable). A sequence that fits one partition is finished by that
+//     workgroup; otherwise each partition writes (running max m, sum l, unnormalised
+//     accumulator) to the workspace and the merge kernel, grid (kv heads, batch), combines
+//     them. The kernel boundary orders the two, so no device-scope fence (an L2 writeback
+//     on this chip) is needed inside a kernel.
+//   * Within a workgroup the wavefronts take turns on "passes" of RPP consecutive keys,
+//     and each wavefront keeps the next pass's K and V loads in flight while it computes
+//     the current one (two register fragments, ping-pong, no copies).
 //     QK: lane (row r, chunk c) holds CH contiguous elements of key r (32-byte loads) and
 //     the matching q slice for all G heads; partial dot products (v_dot2_f32_{bf16,f16} for
 //     16-bit data) are summed across the LPR lanes of a row with xor shuffles.
-//     PV: probabilities and row indices go through a per-wave LDS slot; the value rows are
-//     then read with one dword per lane (a wavefront covers TPI whole rows per load) and
-//     accumulated in fp32 for all G heads.
+//     PV: lane (slot ts, dword u) loads dword u of value rows i*TPI + ts straight from the
+//     pool (a wavefront covers TPI whole rows per load); the probabilities of those rows
+//     come through a per-wavefront LDS slot; accumulation is fp32 for all G heads.
+//   * When a block holds a whole pass (block_size >= RPP) the pass's block id is one scalar
+//     load; otherwise each lane looks its rows up in the table.
 //   * Softmax is online in base 2 with a wave-uniform running max per head that is only
-//     raised when some key exceeds it by more than kRescaleLog2 (then all partial sums are
+//     raised when some key exceeds it by more than kRescaleLog2 (then the partial sums are
 //     rescaled), so most passes need no cross-lane max.
-//   * Partials of a multi-partition sequence (running max m, sum l, unnormalised
-//     accumulator) go to the workspace; the last workgroup of a (sequence, kv head) to
-//     finish (agent-scope counter) merges them and writes the output, then re-arms the
-//     counter to zero. One launch does the whole operation.
 #include <cstdlib>
 #include <cmath>
 
@@ -35,7 +40,7 @@ namespace {
 
 constexpr int kNW = 4;                  // wavefronts per workgroup
 constexpr float kRescaleLog2 = 8.0f;    // lazy-rescale threshold, log2 units (p <= 256)
-constexpr int kDefaultPartTokens = 512;
+constexpr int kDefaultPartTokens = 256;
 
 struct DecodeArgs {
   char* out;
@@ -54,7 +59,6 @@ struct DecodeArgs {
   float scale_log2;
   float* ws_acc;  // [B][Hq][nparts][D]
   float* ws_ml;   // [B][Hq][nparts][2]
-  int* ws_cnt;    // [B][Hkv]
 };
 
 template <int DT, int D, int G>
@@ -68,10 +72,10 @@ struct Shape {
   static constexpr int VPL = ROWDW > kWave ? ROWDW / kWave : 1;      // value dwords per lane
   static constexpr int LPT = ROWDW / VPL;                            // lanes per value row
   static constexpr int TPI = kWave / LPT;                            // value rows per load
+  static constexpr int NV = RPP / TPI;                               // value loads per pass
   static constexpr int VEPL = VPL * 4 / ES;                          // value elements per lane
   static constexpr int GP = (G + 3) & ~3;                            // LDS stride of p rows
   static constexpr int QW = (DT == MIP_F32) ? CH : CH / 2;           // q registers per head
-  static constexpr int PASS_ALIGN = kNW * RPP;
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -93,30 +97,83 @@ __device__ __forceinline__ void load_dwords(uint32_t (&dst)[N], const char* p) {
   }
 }
 
-__device__ __forceinline__ float ws_load(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void ws_store(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// One pass worth of this lane's K/V data (in flight while the previous pass is computed).
+template <int KDW, int NV, int VPL>
+struct PassFrag {
+  uint32_t kw[KDW];
+  uint32_t vw[NV][VPL];
+  bool kvalid;      // this lane's key row is a key of the partition
+  uint32_t vmask;   // bit i: value row i of this lane is a key of the partition
+};
 
 template <int DT, int D, int G>
-__global__ __launch_bounds__(kNW * kWave) void paged_decode_valu(DecodeArgs a) {
+struct Pass {
   using Sh = Shape<DT, D, G>;
+  using Frag = PassFrag<Sh::KDW, Sh::NV, Sh::VPL>;
+
+  // Issue the loads of the pass starting at key `base` (< t1). Rows past t1 are clamped to
+  // the pass's first row (always a key) and flagged invalid; a block id outside the pool
+  // reads block 0 and is flagged invalid, so every address stays inside the pool.
+  static __device__ __forceinline__ void load(Frag& f, const DecodeArgs& a, const int32_t* table, int kvh, int base,
+                                              int t1, int r, int c, int ts, int u) {
+    constexpr int ES = Sh::ES, CH = Sh::CH, RPP = Sh::RPP, KDW = Sh::KDW, ROWDW = Sh::ROWDW;
+    constexpr int VPL = Sh::VPL, TPI = Sh::TPI, NV = Sh::NV;
+    f.vmask = 0u;
+    if (a.bs >= RPP) {
+      const int blk = table[base >> a.log2_bs];
+      const bool bok = blk >= 0 && blk < a.ncb;
+      const int row0 = ((bok ? blk : 0) * a.hkv + kvh) * a.bs + (base & (a.bs - 1));
+      const bool kin = base + r < t1;
+      f.kvalid = bok && kin;
+      load_dwords<KDW>(f.kw, a.k + (static_cast<int64_t>(row0 + (kin ? r : 0)) * D + c * CH) * ES);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int tl = i * TPI + ts;
+        const bool vin = base + tl < t1;
+        f.vmask |= static_cast<uint32_t>(bok && vin) << i;
+        load_dwords<VPL>(f.vw[i], a.v + (static_cast<int64_t>(row0 + (vin ? tl : 0)) * ROWDW + u * VPL) * 4);
+      }
+    } else {
+      {
+        const int tok = base + r < t1 ? base + r : base;
+        const int blk = table[tok >> a.log2_bs];
+        const bool bok = blk >= 0 && blk < a.ncb;
+        f.kvalid = bok && (base + r < t1);
+        const int row = ((bok ? blk : 0) * a.hkv + kvh) * a.bs + (tok & (a.bs - 1));
+        load_dwords<KDW>(f.kw, a.k + (static_cast<int64_t>(row) * D + c * CH) * ES);
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int tl = i * TPI + ts;
+        const int tok = base + tl < t1 ? base + tl : base;
+        const int blk = table[tok >> a.log2_bs];
+        const bool bok = blk >= 0 && blk < a.ncb;
+        f.vmask |= static_cast<uint32_t>(bok && (base + tl < t1)) << i;
+        const int row = ((bok ? blk : 0) * a.hkv + kvh) * a.bs + (tok & (a.bs - 1));
+        load_dwords<VPL>(f.vw[i], a.v + (static_cast<int64_t>(row) * ROWDW + u * VPL) * 4);
+      }
+    }
+  }
+};
+
+template <int DT, int D, int G>
+__global__ __launch_bounds__(kNW * kWave) void paged_decode_part(DecodeArgs a) {
+  using Sh = Shape<DT, D, G>;
+  using P = Pass<DT, D, G>;
+  using Frag = typename P::Frag;
   constexpr int ES = Sh::ES, CH = Sh::CH, LPR = Sh::LPR, RPP = Sh::RPP, KDW = Sh::KDW;
-  constexpr int ROWDW = Sh::ROWDW, VPL = Sh::VPL, LPT = Sh::LPT, TPI = Sh::TPI, VEPL = Sh::VEPL;
+  constexpr int VPL = Sh::VPL, LPT = Sh::LPT, TPI = Sh::TPI, NV = Sh::NV, VEPL = Sh::VEPL;
   constexpr int GP = Sh::GP, QW = Sh::QW;
   using S = typename Elem<DT>::S;
 
   __shared__ float sh_p[kNW][RPP][GP];
-  __shared__ int sh_row[kNW][RPP];
   __shared__ float sh_m[kNW][G];
   __shared__ float sh_l[kNW][G];
   __shared__ float sh_acc[kNW][G][D];
-  __shared__ int sh_last;
 
   const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int h0 = kvh * G;
 
   int ctx = a.lens[b];
@@ -161,37 +218,17 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_valu(DecodeArgs a) {
   const int32_t* table = a.bt + static_cast<int64_t>(b) * a.bt_stride;
   const int ts = lane / LPT, u = lane % LPT;
 
-  for (int base = t0 + w * RPP; base < t1; base += kNW * RPP) {
-    // ---- keys: lane (r, c)
-    const int tok = base + r;
-    bool valid = tok < t1;
-    int row = -1;
-    if (valid) {
-      const int blk = table[tok >> a.log2_bs];
-      if (blk >= 0 && blk < a.ncb) {
-        row = (blk * a.hkv + kvh) * a.bs + (tok & (a.bs - 1));
-      } else {
-        valid = false;
-      }
-    }
-    uint32_t kw[KDW];
-    if (valid) {
-      load_dwords<KDW>(kw, a.k + (static_cast<int64_t>(row) * D + c * CH) * ES);
-    } else {
-#pragma unroll
-      for (int i = 0; i < KDW; ++i) kw[i] = 0u;
-    }
-
+  auto compute = [&](const Frag& f) {
     float s[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float acc_s = 0.0f;
       if constexpr (DT == MIP_F32) {
 #pragma unroll
-        for (int i = 0; i < KDW; ++i) acc_s = fmaf(__uint_as_float(qreg[g][i]), __uint_as_float(kw[i]), acc_s);
+        for (int i = 0; i < KDW; ++i) acc_s = fmaf(__uint_as_float(qreg[g][i]), __uint_as_float(f.kw[i]), acc_s);
       } else {
 #pragma unroll
-        for (int i = 0; i < KDW; ++i) acc_s = dot2<DT>(qreg[g][i], kw[i], acc_s);
+        for (int i = 0; i < KDW; ++i) acc_s = dot2<DT>(qreg[g][i], f.kw[i], acc_s);
       }
       s[g] = acc_s;
     }
@@ -203,7 +240,7 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_valu(DecodeArgs a) {
     bool need = false;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      s[g] = valid ? s[g] * a.scale_log2 : -INFINITY;
+      s[g] = f.kvalid ? s[g] * a.scale_log2 : -INFINITY;
       need |= s[g] > m[g] + kRescaleLog2;
     }
     if (__any(need)) {
@@ -223,42 +260,33 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_valu(DecodeArgs a) {
     float p[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      p[g] = valid ? fast_exp2(s[g] - m[g]) : 0.0f;
+      p[g] = f.kvalid ? fast_exp2(s[g] - m[g]) : 0.0f;
       l[g] += p[g];
     }
     if (c == 0) {
-      sh_row[w][r] = valid ? row : -1;
 #pragma unroll
       for (int g = 0; g < GP; ++g) sh_p[w][r][g] = g < G ? p[g] : 0.0f;
     }
     __builtin_amdgcn_wave_barrier();
-
-    // ---- values: lane (ts, u) covers dwords [u*VPL, u*VPL+VPL) of row i*TPI + ts
 #pragma unroll
-    for (int i = 0; i < RPP / TPI; ++i) {
+    for (int i = 0; i < NV; ++i) {
       const int tl = i * TPI + ts;
-      const int vrow = sh_row[w][tl];
       float pv[GP];
 #pragma unroll
       for (int g4 = 0; g4 < GP / 4; ++g4) {
         const float4 t = *reinterpret_cast<const float4*>(&sh_p[w][tl][4 * g4]);
         pv[4 * g4] = t.x; pv[4 * g4 + 1] = t.y; pv[4 * g4 + 2] = t.z; pv[4 * g4 + 3] = t.w;
       }
-      uint32_t vw[VPL];
-      if (vrow >= 0) {
-        load_dwords<VPL>(vw, a.v + (static_cast<int64_t>(vrow) * ROWDW + u * VPL) * 4);
-      } else {
-#pragma unroll
-        for (int k2 = 0; k2 < VPL; ++k2) vw[k2] = 0u;
-      }
+      const bool ok = (f.vmask >> i) & 1u;
       float vf[VEPL];
 #pragma unroll
       for (int k2 = 0; k2 < VPL; ++k2) {
+        const uint32_t wv = ok ? f.vw[i][k2] : 0u;
         if constexpr (DT == MIP_F32) {
-          vf[k2] = __uint_as_float(vw[k2]);
+          vf[k2] = __uint_as_float(wv);
         } else {
-          vf[2 * k2] = lo16<DT>(vw[k2]);
-          vf[2 * k2 + 1] = hi16<DT>(vw[k2]);
+          vf[2 * k2] = lo16<DT>(wv);
+          vf[2 * k2 + 1] = hi16<DT>(wv);
         }
       }
 #pragma unroll
@@ -268,6 +296,29 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_valu(DecodeArgs a) {
       }
     }
     __builtin_amdgcn_wave_barrier();
+  };
+
+  // ---- software-pipelined pass loop: fragment A/B ping-pong. The next pass is always
+  // loaded (past the end it re-reads the current pass, which stays inside the partition),
+  // so the number of loads in flight is the same on every path and the compiler waits only
+  // for the fragment being computed.
+  constexpr int kStep = kNW * RPP;
+  int base = t0 + w * RPP;
+  if (base < t1) {
+    Frag fa, fb;
+    P::load(fa, a, table, kvh, base, t1, r, c, ts, u);
+    while (true) {
+      int nb = base + kStep;
+      P::load(fb, a, table, kvh, nb < t1 ? nb : base, t1, r, c, ts, u);
+      compute(fa);
+      base = nb;
+      if (base >= t1) break;
+      nb = base + kStep;
+      P::load(fa, a, table, kvh, nb < t1 ? nb : base, t1, r, c, ts, u);
+      compute(fb);
+      base = nb;
+      if (base >= t1) break;
+    }
   }
 
   // ---- wave reduction: l over key rows, acc over value-row slots.
@@ -297,7 +348,7 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_valu(DecodeArgs a) {
   }
   __syncthreads();
 
-  // ---- merge the kNW wavefronts of this workgroup.
+  // ---- merge the kNW wavefronts; finish the sequence or hand the partition to the merge kernel.
   for (int i = tid; i < G * D; i += kNW * kWave) {
     const int g = i / D, d = i % D;
     float mx = -INFINITY;
@@ -315,54 +366,363 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_valu(DecodeArgs a) {
       out_base[b * a.out_sb + (h0 + g) * a.out_sh + d] = from_f32<DT>(Ls > 0.0f ? A / Ls : 0.0f);
     } else {
       const int64_t slot = (static_cast<int64_t>(b) * a.hq + h0 + g) * a.nparts + part;
-      ws_store(a.ws_acc + slot * D + d, A);
+      a.ws_acc[slot * D + d] = A;
       if (d == 0) {
-        ws_store(a.ws_ml + slot * 2, mx);
-        ws_store(a.ws_ml + slot * 2 + 1, Ls);
+        a.ws_ml[slot * 2] = mx;
+        a.ws_ml[slot * 2 + 1] = Ls;
       }
     }
   }
-  if (np_b == 1) return;
+}
 
-  // ---- cross-workgroup merge by the last partition to finish.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int prev = atomicAdd(a.ws_cnt + b * a.hkv + kvh, 1);
-    sh_last = (prev == np_b - 1);
+// ---------------------------------------------------------------- MFMA partition kernel
+//
+// For 16-bit K/V with head_dim 64 or 128 and up to 16 query heads per kv head. Same grid,
+// partitions, workspace and merge kernel as the VALU kernel; the inner tile is different.
+// A tile is 16 consecutive keys of one wavefront:
+//   S^T[16 keys x 16 heads] = K[16 x D] . Q^T[D x 16]       v_mfma_f32_16x16x32_{bf16,f16}
+//       A = key rows as loaded (lane l: key l%16, dims 8*(l/16)+32*kc .. +7, one 16-byte load),
+//       B = q (lane l: head l%16, same dims), zero for heads >= G;
+//       out: lane l holds keys 4*(l/16)+i (i = 0..3) of head l%16.
+//   O^T[D x 16 heads] += V^T[D x 16 keys] . P^T[16 keys x 16 heads]   v_mfma_f32_16x16x16_*
+//       B = P^T is exactly the S^T output layout, so probabilities stay in registers;
+//       A = V^T: lane l needs keys 4*(l/16)+i at dim l%16 (+16 per M-tile), read from a
+//       per-wavefront LDS copy of the value tile (written from the 16-byte row loads);
+//       P is split into hi + lo 16-bit parts (two MFMAs) so PV keeps ~fp32 precision.
+// Every (dim, head) accumulator lives in exactly one lane, and a lane only ever rescales
+// its own head, so the running max/sum need no cross-lane traffic except on a rescale.
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+template <int DT> struct MfmaOps;
+template <> struct MfmaOps<MIP_BF16> {
+  static __device__ __forceinline__ f32x4_t qk(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t pv(uint2 a, uint2 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b),
+                                                     c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t round16(float x) { return f32_to_bf16_rne(x); }
+  static __device__ __forceinline__ float widen16(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+};
+template <> struct MfmaOps<MIP_F16> {
+  static __device__ __forceinline__ f32x4_t qk(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t pv(uint2 a, uint2 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c,
+                                                 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t round16(float x) { return f32_to_f16_rne(x); }
+  static __device__ __forceinline__ float widen16(uint16_t h) { return f16_bits_to_f32(h); }
+};
+
+template <int D>
+struct MShape {
+  static constexpr int KC = D / 32;                 // 16-byte loads per lane per tile row, QK K-steps
+  static constexpr int MT = D / 16;                 // O^T M-tiles
+  static constexpr int TPW = D <= 64 ? 2 : 1;       // tiles per pass (8 KB of K+V per pass in flight)
+  static constexpr int PASS = 16 * TPW;             // keys per pass
+  static constexpr int TILE_BYTES = 16 * D * 2;
+};
+
+template <int D>
+struct MFrag {
+  uint4 k[MShape<D>::TPW][MShape<D>::KC];
+  uint4 v[MShape<D>::TPW][MShape<D>::KC];
+  uint32_t rowok;  // bit t: this lane's row (key l%16) of tile t is a key of the partition
+};
+
+// Load one pass (TPW tiles) starting at key `base` (< t1). Lane l loads key row l%16 of each
+// tile; rows past t1 re-read the tile's first key, rows of an invalid block id read block 0,
+// so every address stays inside the pool; both are flagged in rowok.
+template <int D>
+__device__ __forceinline__ void mfma_load_rows(MFrag<D>& f, const DecodeArgs& a, int t, int64_t row, int grp) {
+  const char* kp = a.k + row * (D * 2) + 16 * grp;
+  const char* vp = a.v + row * (D * 2) + 16 * grp;
+#pragma unroll
+  for (int kc = 0; kc < MShape<D>::KC; ++kc) {
+    f.k[t][kc] = *reinterpret_cast<const uint4*>(kp + 64 * kc);
+    f.v[t][kc] = *reinterpret_cast<const uint4*>(vp + 64 * kc);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void mfma_load(MFrag<D>& f, const DecodeArgs& a, const int32_t* table, int kvh, int base,
+                                          int t1, int i16, int grp) {
+  using MS = MShape<D>;
+  f.rowok = 0u;
+  if (a.bs >= 16) {
+    // A tile never crosses a block: one scalar table load per tile, so the row loads wait
+    // only on the scalar counter and the previous pass's loads stay in flight.
+#pragma unroll
+    for (int t = 0; t < MS::TPW; ++t) {
+      const int tb = __builtin_amdgcn_readfirstlane(base + 16 * t < t1 ? base + 16 * t : base);
+      const int blk = __builtin_amdgcn_readfirstlane(table[tb >> a.log2_bs]);
+      const bool bok = blk >= 0 && blk < a.ncb;
+      const int tok = base + 16 * t + i16;
+      const bool in = tok < t1;
+      const int off = ((in ? tok : tb) & (a.bs - 1));
+      f.rowok |= static_cast<uint32_t>(in && bok) << t;
+      mfma_load_rows<D>(f, a, t, static_cast<int64_t>(((bok ? blk : 0) * a.hkv + kvh) * a.bs + off), grp);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < MS::TPW; ++t) {
+      const int tb = base + 16 * t;
+      const int tok = tb + i16;
+      const bool in = tok < t1;
+      const int tk = in ? tok : (tb < t1 ? tb : base);
+      const int blk = table[tk >> a.log2_bs];
+      const bool bok = blk >= 0 && blk < a.ncb;
+      f.rowok |= static_cast<uint32_t>(in && bok) << t;
+      mfma_load_rows<D>(f, a, t, static_cast<int64_t>(((bok ? blk : 0) * a.hkv + kvh) * a.bs + (tk & (a.bs - 1))),
+                        grp);
+    }
+  }
+}
+
+template <int DT, int D, int G>
+__global__ __launch_bounds__(kNW * kWave) void paged_decode_part_mfma(DecodeArgs a) {
+  using MS = MShape<D>;
+  using Ops = MfmaOps<DT>;
+  using S = typename Elem<DT>::S;
+  constexpr int KC = MS::KC, MT = MS::MT, TPW = MS::TPW, PASS = MS::PASS;
+  constexpr int LDS_TILES = kNW * TPW * MS::TILE_BYTES;
+  constexpr int LDS_MERGE = (kNW * G * D + 2 * kNW * 16) * 4;
+  constexpr int LDS_BYTES = LDS_TILES > LDS_MERGE ? LDS_TILES : LDS_MERGE;
+  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
+
+  const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int i16 = lane & 15, grp = lane >> 4;
+  const int h0 = kvh * G;
+
+  int ctx = a.lens[b];
+  const int cap = a.max_blocks * a.bs;
+  ctx = ctx < cap ? ctx : cap;
+  const int np_b = ctx > 0 ? (ctx + a.part_tokens - 1) / a.part_tokens : 1;
+  if (part >= np_b) return;
+  S* out_base = reinterpret_cast<S*>(a.out);
+  if (ctx <= 0) {
+    for (int i = tid; i < G * D; i += kNW * kWave) {
+      const int g = i / D, d = i % D;
+      out_base[b * a.out_sb + (h0 + g) * a.out_sh + d] = from_f32<DT>(0.0f);
+    }
+    return;
+  }
+  const int t0 = part * a.part_tokens;
+  const int t1 = (t0 + a.part_tokens < ctx) ? t0 + a.part_tokens : ctx;
+
+  // Q^T operand: lane l holds q[head l%16][dims 32*kc + 8*(l/16) .. +7], zero past G.
+  uint4 qb[KC];
+  {
+    const char* qrow = a.q + (static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(h0 + i16) * a.q_sh) * 2;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+      qb[kc] = i16 < G ? *reinterpret_cast<const uint4*>(qrow + 64 * kc + 16 * grp) : make_uint4(0, 0, 0, 0);
+  }
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -INFINITY, l = 0.0f;
+  const bool head_live = i16 < G;
+  const int32_t* table = a.bt + static_cast<int64_t>(b) * a.bt_stride;
+  char* my_tiles = smem + w * TPW * MS::TILE_BYTES;
+
+  auto compute = [&](const MFrag<D>& f, int base) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tb = base + 16 * t;
+      const bool ok_row = (f.rowok >> t) & 1u;
+      // Value rows into this wavefront's LDS tile (zeros for rows that are not keys).
+      char* tile = my_tiles + t * MS::TILE_BYTES;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const uint4 vv = ok_row ? f.v[t][kc] : make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(tile + i16 * (D * 2) + 64 * kc + 16 * grp) = vv;
+      }
+      // Keys valid as rows of the S^T output: row j = 4*grp + i is a key iff lane j's row was.
+      const uint32_t okmask = static_cast<uint32_t>(__ballot(ok_row)) & 0xffffu;
+      f32x4_t st = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) st = Ops::qk(f.k[t][kc], qb[kc], st);
+      float sv[4];
+      bool need = false;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = head_live && ((okmask >> (4 * grp + i)) & 1u) && (tb + 4 * grp + i < t1);
+        sv[i] = ok ? st[i] * a.scale_log2 : -INFINITY;
+        need |= sv[i] > m + kRescaleLog2;
+      }
+      if (__any(need)) {
+        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float alpha = (m == -INFINITY) ? 0.0f : fast_exp2(m - mn);
+        l *= alpha;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] *= alpha;
+        m = mn;
+      }
+      uint32_t ph[2], pl[2];
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        const float p0 = sv[i] == -INFINITY ? 0.0f : fast_exp2(sv[i] - m);
+        const float p1 = sv[i + 1] == -INFINITY ? 0.0f : fast_exp2(sv[i + 1] - m);
+        l += p0 + p1;
+        const uint16_t h0b = Ops::round16(p0), h1b = Ops::round16(p1);
+        const uint16_t l0b = Ops::round16(p0 - Ops::widen16(h0b)), l1b = Ops::round16(p1 - Ops::widen16(h1b));
+        ph[i / 2] = static_cast<uint32_t>(h0b) | (static_cast<uint32_t>(h1b) << 16);
+        pl[i / 2] = static_cast<uint32_t>(l0b) | (static_cast<uint32_t>(l1b) << 16);
+      }
+      __builtin_amdgcn_wave_barrier();
+      // V^T operand: lane l takes keys 4*grp + i at dim 16*mt + i16.
+      const uint16_t* tv = reinterpret_cast<const uint16_t*>(tile) + (4 * grp) * D + i16;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint32_t e0 = tv[16 * mt], e1 = tv[D + 16 * mt], e2 = tv[2 * D + 16 * mt], e3 = tv[3 * D + 16 * mt];
+        const uint2 va = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+        acc[mt] = Ops::pv(va, make_uint2(ph[0], ph[1]), acc[mt]);
+        acc[mt] = Ops::pv(va, make_uint2(pl[0], pl[1]), acc[mt]);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  };
+
+  constexpr int kStep = kNW * PASS;
+  int base = t0 + w * PASS;
+  if (base < t1) {
+    MFrag<D> fa, fb;
+    mfma_load<D>(fa, a, table, kvh, base, t1, i16, grp);
+    while (true) {
+      int nb = base + kStep;
+      mfma_load<D>(fb, a, table, kvh, nb < t1 ? nb : base, t1, i16, grp);
+      compute(fa, base);
+      base = nb;
+      if (base >= t1) break;
+      nb = base + kStep;
+      mfma_load<D>(fa, a, table, kvh, nb < t1 ? nb : base, t1, i16, grp);
+      compute(fb, base);
+      base = nb;
+      if (base >= t1) break;
+    }
+  }
+
+  // ---- per-wave totals: l summed over the 4 lane groups; acc needs no reduction.
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  __syncthreads();  // the merge area overlaps other wavefronts' value tiles
+  float* sh_acc = reinterpret_cast<float*>(smem);          // [kNW][G][D]
+  float* sh_m = sh_acc + kNW * G * D;                       // [kNW][16]
+  float* sh_l = sh_m + kNW * 16;                            // [kNW][16]
+  if (head_live) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sh_acc[(w * G + i16) * D + 16 * mt + 4 * grp + i] = acc[mt][i];
+    }
+    if (grp == 0) {
+      sh_m[w * 16 + i16] = m;
+      sh_l[w * 16 + i16] = l;
+    }
   }
   __syncthreads();
-  if (!sh_last) return;
-  __threadfence();
   for (int i = tid; i < G * D; i += kNW * kWave) {
+    const int g = i / D, d = i % D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kNW; ++ww) mx = fmaxf(mx, sh_m[ww * 16 + g]);
+    float A = 0.0f, Ls = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < kNW; ++ww) {
+      const float mw = sh_m[ww * 16 + g];
+      const float wt = (mw == -INFINITY) ? 0.0f : fast_exp2(mw - mx);
+      A = fmaf(wt, sh_acc[(ww * G + g) * D + d], A);
+      Ls = fmaf(wt, sh_l[ww * 16 + g], Ls);
+    }
+    if (np_b == 1) {
+      out_base[b * a.out_sb + (h0 + g) * a.out_sh + d] = from_f32<DT>(Ls > 0.0f ? A / Ls : 0.0f);
+    } else {
+      const int64_t slot = (static_cast<int64_t>(b) * a.hq + h0 + g) * a.nparts + part;
+      a.ws_acc[slot * D + d] = A;
+      if (d == 0) {
+        a.ws_ml[slot * 2] = mx;
+        a.ws_ml[slot * 2 + 1] = Ls;
+      }
+    }
+  }
+}
+
+// Combine the partitions of every sequence that needed more than one. Grid (kv heads, batch).
+template <int DT, int D, int G>
+__global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
+  using S = typename Elem<DT>::S;
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  int ctx = a.lens[b];
+  const int cap = a.max_blocks * a.bs;
+  ctx = ctx < cap ? ctx : cap;
+  const int np_b = ctx > 0 ? (ctx + a.part_tokens - 1) / a.part_tokens : 1;
+  if (np_b <= 1) return;
+  S* out_base = reinterpret_cast<S*>(a.out);
+  const int h0 = kvh * G;
+  for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
     const int g = i / D, d = i % D;
     const int64_t slot0 = (static_cast<int64_t>(b) * a.hq + h0 + g) * a.nparts;
     float mx = -INFINITY;
-    for (int pp = 0; pp < np_b; ++pp) mx = fmaxf(mx, ws_load(a.ws_ml + (slot0 + pp) * 2));
+    for (int pp = 0; pp < np_b; ++pp) mx = fmaxf(mx, a.ws_ml[(slot0 + pp) * 2]);
     float A = 0.0f, Ls = 0.0f;
     for (int pp = 0; pp < np_b; ++pp) {
-      const float mp = ws_load(a.ws_ml + (slot0 + pp) * 2);
+      const float mp = a.ws_ml[(slot0 + pp) * 2];
       const float wt = (mp == -INFINITY) ? 0.0f : fast_exp2(mp - mx);
-      A = fmaf(wt, ws_load(a.ws_acc + (slot0 + pp) * D + d), A);
-      Ls = fmaf(wt, ws_load(a.ws_ml + (slot0 + pp) * 2 + 1), Ls);
+      A = fmaf(wt, a.ws_acc[(slot0 + pp) * D + d], A);
+      Ls = fmaf(wt, a.ws_ml[(slot0 + pp) * 2 + 1], Ls);
     }
     out_base[b * a.out_sb + (h0 + g) * a.out_sh + d] = from_f32<DT>(Ls > 0.0f ? A / Ls : 0.0f);
   }
-  if (tid == 0) __hip_atomic_store(a.ws_cnt + b * a.hkv + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------ host side
 
 inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
-int rows_per_pass(int dtype, int d) {
+enum class Algo { kValu, kMfma };
+
+bool mfma_eligible(int dtype, int d, int g) {
+  return (dtype == MIP_BF16 || dtype == MIP_F16) && (d == 64 || d == 128) && g >= 1 && g <= 16;
+}
+
+// MFMA for 16-bit data at head_dim 64/128 (the faster kernel under rocprof at the Qwen
+// shapes); the VALU kernel covers fp32 and the other head sizes. MIP_DECODE_ALGO=valu|mfma
+// forces one of them (diagnostics and the kernel comparison).
+Algo choose_algo(int dtype, int d, int g) {
+  const char* env = std::getenv("MIP_DECODE_ALGO");
+  const int forced = !env ? 0 : env[0] == 'v' ? 1 : env[0] == 'm' ? 2 : 0;
+  const bool mfma_ok = mfma_eligible(dtype, d, g);
+  if (forced == 1 && g <= 8) return Algo::kValu;
+  if (forced == 2 && mfma_ok) return Algo::kMfma;
+  return mfma_ok ? Algo::kMfma : Algo::kValu;
+}
+
+int pass_tokens(Algo algo, int dtype, int d) {
+  if (algo == Algo::kMfma) return d <= 64 ? 32 : 16;
   const int es = dtype == MIP_F32 ? 4 : 2;
   const int ch = d < 32 / es ? d : 32 / es;
   return kWave / (d / ch);
 }
 
-int part_tokens_for(int dtype, int d) {
-  const int align = kNW * rows_per_pass(dtype, d);
+int part_tokens_for(Algo algo, int dtype, int d) {
+  const int align = kNW * pass_tokens(algo, dtype, d);
   int want = kDefaultPartTokens;
   if (const char* env = std::getenv("MIP_PART_TOKENS")) {
     const int v = std::atoi(env);
@@ -372,60 +732,115 @@ int part_tokens_for(int dtype, int d) {
 }
 
 struct WsLayout {
+  Algo algo;
+  int part_tokens;
   int nparts;
-  int64_t cnt_off, ml_off, acc_off, bytes;
+  int64_t ml_off, acc_off, bytes;
 };
 
 WsLayout ws_layout(int batch, int hq, int hkv, int d, int bs, int max_blocks, int dtype) {
   WsLayout w{};
-  const int pt = part_tokens_for(dtype, d);
+  w.algo = choose_algo(dtype, d, hq / hkv);
+  w.part_tokens = part_tokens_for(w.algo, dtype, d);
   const int64_t max_ctx = static_cast<int64_t>(max_blocks) * bs;
-  w.nparts = static_cast<int>((max_ctx + pt - 1) / pt);
+  w.nparts = static_cast<int>((max_ctx + w.part_tokens - 1) / w.part_tokens);
   if (w.nparts < 1) w.nparts = 1;
   if (w.nparts == 1) return w;
-  w.cnt_off = 0;
-  w.ml_off = align_up(static_cast<int64_t>(batch) * hkv * 4, 256);
-  w.acc_off = w.ml_off + align_up(static_cast<int64_t>(batch) * hq * w.nparts * 2 * 4, 256);
+  w.ml_off = 0;
+  w.acc_off = align_up(static_cast<int64_t>(batch) * hq * w.nparts * 2 * 4, 256);
   w.bytes = w.acc_off + align_up(static_cast<int64_t>(batch) * hq * w.nparts * d * 4, 256);
   return w;
 }
 
 using KernelFn = void (*)(DecodeArgs);
+struct KernelPair {
+  KernelFn part = nullptr;
+  KernelFn merge = nullptr;
+};
+
+template <int DT, int D, int G>
+KernelPair valu_pair() {
+  return {paged_decode_part<DT, D, G>, paged_decode_merge<DT, D, G>};
+}
 
 template <int DT, int D>
-KernelFn pick_g(int g) {
+KernelPair pick_valu_g(int g) {
   switch (g) {
-    case 1: return paged_decode_valu<DT, D, 1>;
-    case 2: return paged_decode_valu<DT, D, 2>;
-    case 3: return paged_decode_valu<DT, D, 3>;
-    case 4: return paged_decode_valu<DT, D, 4>;
-    case 5: return paged_decode_valu<DT, D, 5>;
-    case 6: return paged_decode_valu<DT, D, 6>;
-    case 7: return paged_decode_valu<DT, D, 7>;
-    case 8: return paged_decode_valu<DT, D, 8>;
-    default: return nullptr;
+    case 1: return valu_pair<DT, D, 1>();
+    case 2: return valu_pair<DT, D, 2>();
+    case 3: return valu_pair<DT, D, 3>();
+    case 4: return valu_pair<DT, D, 4>();
+    case 5: return valu_pair<DT, D, 5>();
+    case 6: return valu_pair<DT, D, 6>();
+    case 7: return valu_pair<DT, D, 7>();
+    case 8: return valu_pair<DT, D, 8>();
+    default: return {};
   }
 }
 
 template <int DT>
-KernelFn pick_d(int d, int g) {
+KernelPair pick_valu_d(int d, int g) {
   switch (d) {
-    case 8: return pick_g<DT, 8>(g);
-    case 16: return pick_g<DT, 16>(g);
-    case 32: return pick_g<DT, 32>(g);
-    case 64: return pick_g<DT, 64>(g);
-    case 128: return pick_g<DT, 128>(g);
-    case 256: return pick_g<DT, 256>(g);
-    default: return nullptr;
+    case 8: return pick_valu_g<DT, 8>(g);
+    case 16: return pick_valu_g<DT, 16>(g);
+    case 32: return pick_valu_g<DT, 32>(g);
+    case 64: return pick_valu_g<DT, 64>(g);
+    case 128: return pick_valu_g<DT, 128>(g);
+    case 256: return pick_valu_g<DT, 256>(g);
+    default: return {};
   }
 }
 
-KernelFn pick_kernel(int dtype, int d, int g) {
+template <int DT, int D, int G>
+KernelPair mfma_pair() {
+  return {paged_decode_part_mfma<DT, D, G>, paged_decode_merge<DT, D, G>};
+}
+
+template <int DT, int D>
+KernelPair pick_mfma_g(int g) {
+  switch (g) {
+    case 1: return mfma_pair<DT, D, 1>();
+    case 2: return mfma_pair<DT, D, 2>();
+    case 3: return mfma_pair<DT, D, 3>();
+    case 4: return mfma_pair<DT, D, 4>();
+    case 5: return mfma_pair<DT, D, 5>();
+    case 6: return mfma_pair<DT, D, 6>();
+    case 7: return mfma_pair<DT, D, 7>();
+    case 8: return mfma_pair<DT, D, 8>();
+    case 9: return mfma_pair<DT, D, 9>();
+    case 10: return mfma_pair<DT, D, 10>();
+    case 11: return mfma_pair<DT, D, 11>();
+    case 12: return mfma_pair<DT, D, 12>();
+    case 13: return mfma_pair<DT, D, 13>();
+    case 14: return mfma_pair<DT, D, 14>();
+    case 15: return mfma_pair<DT, D, 15>();
+    case 16: return mfma_pair<DT, D, 16>();
+    default: return {};
+  }
+}
+
+template <int DT>
+KernelPair pick_mfma_d(int d, int g) {
+  switch (d) {
+    case 64: return pick_mfma_g<DT, 64>(g);
+    case 128: return pick_mfma_g<DT, 128>(g);
+    default: return {};
+  }
+}
+
+KernelPair pick_kernel(Algo algo, int dtype, int d, int g) {
+  if (algo == Algo::kMfma) {
+    switch (dtype) {
+      case MIP_F16: return pick_mfma_d<MIP_F16>(d, g);
+      case MIP_BF16: return pick_mfma_d<MIP_BF16>(d, g);
+      default: return {};
+    }
+  }
   switch (dtype) {
-    case MIP_F32: return pick_d<MIP_F32>(d, g);
-    case MIP_F16: return pick_d<MIP_F16>(d, g);
-    case MIP_BF16: return pick_d<MIP_BF16>(d, g);
-    default: return nullptr;
+    case MIP_F32: return pick_valu_d<MIP_F32>(d, g);
+    case MIP_F16: return pick_valu_d<MIP_F16>(d, g);
+    case MIP_BF16: return pick_valu_d<MIP_BF16>(d, g);
+    default: return {};
   }
 }
 
@@ -460,25 +875,25 @@ extern "C" int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_str
   if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens) return MIP_EINVAL;
   if (!std::isfinite(scale)) return MIP_EINVAL;
   const int group = num_heads / num_kv_heads;
-  KernelFn fn = pick_kernel(dtype, head_dim, group);
-  if (!fn) return MIP_EUNSUPPORTED;
+  const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
+  const KernelPair kp = pick_kernel(wl.algo, dtype, head_dim, group);
+  if (!kp.part) return MIP_EUNSUPPORTED;
   const int64_t es = dtype == MIP_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return MIP_EINVAL;
+  const uint64_t q_align = wl.algo == Algo::kMfma ? 15 : 3;  // MFMA reads q rows with 16-byte loads
   if ((reinterpret_cast<uintptr_t>(q) | static_cast<uint64_t>(q_stride_b * es) |
-       static_cast<uint64_t>(q_stride_h * es)) & 3)
+       static_cast<uint64_t>(q_stride_h * es)) & q_align)
     return MIP_EINVAL;
   if ((reinterpret_cast<uintptr_t>(out) | static_cast<uint64_t>(out_stride_b * es) |
        static_cast<uint64_t>(out_stride_h * es)) & (es - 1))
     return MIP_EINVAL;
 
-  const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
   DecodeArgs a{};
   if (wl.nparts > 1) {
     if (!workspace || workspace_bytes < static_cast<size_t>(wl.bytes) ||
         (reinterpret_cast<uintptr_t>(workspace) & 255))
       return MIP_EINVAL;
     char* ws = static_cast<char*>(workspace);
-    a.ws_cnt = reinterpret_cast<int*>(ws + wl.cnt_off);
     a.ws_ml = reinterpret_cast<float*>(ws + wl.ml_off);
     a.ws_acc = reinterpret_cast<float*>(ws + wl.acc_off);
   }
@@ -499,11 +914,12 @@ extern "C" int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_str
   a.bs = block_size;
   a.log2_bs = ilog2_exact(block_size);
   a.max_blocks = max_blocks_per_seq;
-  a.part_tokens = part_tokens_for(dtype, head_dim);
+  a.part_tokens = wl.part_tokens;
   a.nparts = wl.nparts;
   a.scale_log2 = scale * 1.4426950408889634f;
   if (batch > 65535) return MIP_EINVAL;
-  hipLaunchKernelGGL(fn, dim3(wl.nparts, num_kv_heads, batch), dim3(kNW * kWave), 0,
-                     static_cast<hipStream_t>(stream), a);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(kp.part, dim3(wl.nparts, num_kv_heads, batch), dim3(kNW * kWave), 0, s, a);
+  if (wl.nparts > 1) hipLaunchKernelGGL(kp.merge, dim3(num_kv_heads, batch), dim3(256), 0, s, a);
   return status_from_hip(hipGetLastError());
 }

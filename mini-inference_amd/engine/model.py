@@ -179,14 +179,15 @@ class Qwen2ForCausalLM(nn.Module):
 
 
 def random_init_(model: Qwen2ForCausalLM, seed: int = 0, std: float = 0.02) -> Qwen2ForCausalLM:
-    """Fill every weight from a seeded normal (norm weights stay 1): no checkpoint needed."""
-    gen = torch.Generator(device="cpu").manual_seed(seed)
+    """Fill every weight in place from a seeded normal on its own device (norm weights stay 1)."""
+    dev = next(model.parameters()).device
+    gen = torch.Generator(device=dev).manual_seed(seed)
     with torch.no_grad():
         for name, p in model.named_parameters():
             if name.endswith("norm.weight"):
                 p.fill_(1.0)
             else:
-                p.copy_(torch.randn(p.shape, generator=gen) * std)
+                p.normal_(0.0, std, generator=gen)
     return model
 
 

@@ -36,15 +36,32 @@ def _stream_ptr(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-              slot_mapping: torch.Tensor) -> None:
-    """Write token i's K/V rows (``k[i, h, :]``) to pool slot ``slot_mapping[i]``.
+class PreparedCall:
+    """One validated C-ABI call with its argument tuple fixed (pointers, strides, stream).
 
-    ``k_cache``/``v_cache``: one layer of the pool, ``[num_blocks + 1, Hkv, block_size, D]``
-    contiguous. ``k``/``v``: ``[N, Hkv, D]`` with any token/head strides and a contiguous
-    last dimension. ``slot_mapping``: int64 ``[N]``, ``block * block_size + offset``.
-    Follows engine/kv_cache.py:613-614 and :286-289 (bit-exact data movement).
+    Calling it re-launches the kernel on the same buffers with no Python-side checks, for
+    loops over static buffers (graph capture, timing). The tensors passed to the
+    ``prepare_*`` function must stay alive and in place while it is used.
     """
+
+    __slots__ = ("_fn", "_args", "_what", "keep")
+
+    def __init__(self, fn, args: tuple, what: str, keep: tuple = ()) -> None:
+        self._fn, self._args, self._what, self.keep = fn, args, what, keep
+
+    def __call__(self) -> None:
+        st = self._fn(*self._args)
+        if st:
+            _native.check(st, self._what)
+
+
+def _noop() -> None:
+    return None
+
+
+def prepare_kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      slot_mapping: torch.Tensor):
+    """Validate a :func:`kv_append` call once; returns a :class:`PreparedCall` (or a no-op for N = 0)."""
     _require_device(k_cache, v_cache, k, v, slot_mapping)
     if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("k_cache/v_cache must be contiguous [num_blocks, Hkv, block_size, D] tensors of one shape")
@@ -61,14 +78,24 @@ def kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: 
         raise ValueError("slot_mapping must be contiguous")
     n = k.shape[0]
     if n == 0:
-        return
+        return _noop
     lib = _native.load()
-    st = lib.mip_kv_append(
-        k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
-        k_cache.data_ptr(), v_cache.data_ptr(), nb, slot_mapping.data_ptr(), n, hkv, d, bs,
-        dtype_code(k_cache.dtype), _stream_ptr(k_cache.device),
-    )
-    _native.check(st, "mip_kv_append")
+    args = (k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+            k_cache.data_ptr(), v_cache.data_ptr(), nb, slot_mapping.data_ptr(), n, hkv, d, bs,
+            dtype_code(k_cache.dtype), _stream_ptr(k_cache.device))
+    return PreparedCall(lib.mip_kv_append, args, "mip_kv_append", (k_cache, v_cache, k, v, slot_mapping))
+
+
+def kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+              slot_mapping: torch.Tensor) -> None:
+    """Write token i's K/V rows (``k[i, h, :]``) to pool slot ``slot_mapping[i]``.
+
+    ``k_cache``/``v_cache``: one layer of the pool, ``[num_blocks + 1, Hkv, block_size, D]``
+    contiguous. ``k``/``v``: ``[N, Hkv, D]`` with any token/head strides and a contiguous
+    last dimension. ``slot_mapping``: int64 ``[N]``, ``block * block_size + offset``.
+    Follows engine/kv_cache.py:613-614 and :286-289 (bit-exact data movement).
+    """
+    prepare_kv_append(k_cache, v_cache, k, v, slot_mapping)()
 
 
 class _Workspace:
@@ -105,17 +132,10 @@ def decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_d
                                                          max_blocks, dtype_code(dtype)))
 
 
-def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
-                 context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
-                 max_blocks: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """Decode attention over paged K/V for one query token per sequence.
-
-    ``q``: ``[B, Hq, D]`` (last dim contiguous). ``k_cache``/``v_cache``: one layer,
-    ``[num_blocks + 1, Hkv, block_size, D]``. ``block_tables``: int32 ``[B, >= max_blocks]``.
-    ``context_lens``: int32 ``[B]`` (keys attended = positions + 1). Returns ``out``
-    ``[B, Hq, D]`` in q's dtype. Follows engine/kv_cache.py:615-620 and
-    engine/model.py:126-147 with ``scale = 1/sqrt(D)`` by default.
-    """
+def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                         context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
+                         max_blocks: int | None = None, workspace: torch.Tensor | None = None):
+    """Validate a :func:`paged_decode` call once; returns ``(PreparedCall, out)``."""
     _require_device(q, k_cache, v_cache, block_tables, context_lens)
     if q.dim() != 3 or q.stride(2) != 1:
         raise ValueError("q must be [B, Hq, D] with a contiguous last dimension")
@@ -141,7 +161,7 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     elif out.shape != (b, hq, d) or out.dtype != q.dtype or out.stride(2) != 1:
         raise ValueError("out must be [B, Hq, D] in q's dtype with a contiguous last dimension")
     if b == 0:
-        return out
+        return _noop, out
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
     code = dtype_code(q.dtype)
     lib = _native.load()
@@ -152,12 +172,27 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
         raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, needs {need}")
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    st = lib.mip_paged_decode(
-        out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1),
-        k_cache.data_ptr(), v_cache.data_ptr(), nb, block_tables.data_ptr(), block_tables.stride(0),
-        context_lens.data_ptr(), b, hq, hkv, d, bs, mb, scale, ws_ptr, ws_bytes, code, _stream_ptr(q.device),
-    )
-    _native.check(st, "mip_paged_decode")
+    args = (out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1),
+            k_cache.data_ptr(), v_cache.data_ptr(), nb, block_tables.data_ptr(), block_tables.stride(0),
+            context_lens.data_ptr(), b, hq, hkv, d, bs, mb, scale, ws_ptr, ws_bytes, code, _stream_ptr(q.device))
+    keep = (out, q, k_cache, v_cache, block_tables, context_lens, workspace)
+    return PreparedCall(lib.mip_paged_decode, args, "mip_paged_decode", keep), out
+
+
+def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                 context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
+                 max_blocks: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention over paged K/V for one query token per sequence.
+
+    ``q``: ``[B, Hq, D]`` (last dim contiguous). ``k_cache``/``v_cache``: one layer,
+    ``[num_blocks + 1, Hkv, block_size, D]``. ``block_tables``: int32 ``[B, >= max_blocks]``.
+    ``context_lens``: int32 ``[B]`` (keys attended = positions + 1). Returns ``out``
+    ``[B, Hq, D]`` in q's dtype. Follows engine/kv_cache.py:615-620 and
+    engine/model.py:126-147 with ``scale = 1/sqrt(D)`` by default.
+    """
+    call, out = prepare_paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, out, max_blocks,
+                                     workspace)
+    call()
     return out
 
 
