@@ -33,6 +33,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # Packed fp32 VALU ops (v_pk_fma_f32 and friends) stay disabled for every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs (the softmax rescale and the epilogue work on them with VALU
+    # ops; AGPR placement costs a copy each way per tile).
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
 ]
 

@@ -4,7 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/mipaged.h"
+#include "mipaged.h"
 
 namespace mip {
 
@@ -56,6 +56,13 @@ template <> __device__ __forceinline__ float dot2<MIP_BF16>(uint32_t a, uint32_t
 }
 template <> __device__ __forceinline__ float dot2<MIP_F16>(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+}
+
+// Read a wave-uniform int32 through the constant address space, so it becomes a scalar load
+// (its own counter) even in kernels that store to global memory. Only for inputs that no
+// kernel writes while it runs (block tables).
+__device__ __forceinline__ int load_uniform_i32(const int32_t* p) {
+  return *(const __attribute__((address_space(4))) int32_t*)(p);
 }
 
 __host__ __device__ constexpr int ilog2_exact(int x) { return x <= 1 ? 0 : 1 + ilog2_exact(x >> 1); }

@@ -31,35 +31,17 @@
 //     raised when some key exceeds it by more than kRescaleLog2 (then the partial sums are
 //     rescaled), so most passes need no cross-lane max.
 #include <cstdlib>
+#include <type_traits>
 #include <cmath>
 
-#include "mip_common.h"
+#include "paged_decode_common.h"
 
 namespace mip {
 namespace {
 
-constexpr int kNW = 4;                  // wavefronts per workgroup
-constexpr float kRescaleLog2 = 8.0f;    // lazy-rescale threshold, log2 units (p <= 256)
-constexpr int kDefaultPartTokens = 256;
+using namespace decode;
 
-struct DecodeArgs {
-  char* out;
-  int64_t out_sb, out_sh;  // elements
-  const char* q;
-  int64_t q_sb, q_sh;      // elements
-  const char* k;
-  const char* v;
-  int64_t ncb;
-  const int32_t* bt;
-  int64_t bt_stride;
-  const int32_t* lens;
-  int hq, hkv, bs, log2_bs, max_blocks;
-  int part_tokens;
-  int nparts;
-  float scale_log2;
-  float* ws_acc;  // [B][Hq][nparts][D]
-  float* ws_ml;   // [B][Hq][nparts][2]
-};
+constexpr int kDefaultPartTokens = 256;
 
 template <int DT, int D, int G>
 struct Shape {
@@ -77,8 +59,6 @@ struct Shape {
   static constexpr int GP = (G + 3) & ~3;                            // LDS stride of p rows
   static constexpr int QW = (DT == MIP_F32) ? CH : CH / 2;           // q registers per head
 };
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int N>
 __device__ __forceinline__ void load_dwords(uint32_t (&dst)[N], const char* p) {
@@ -120,7 +100,7 @@ struct Pass {
     constexpr int VPL = Sh::VPL, TPI = Sh::TPI, NV = Sh::NV;
     f.vmask = 0u;
     if (a.bs >= RPP) {
-      const int blk = table[base >> a.log2_bs];
+      const int blk = load_uniform_i32(table + (base >> a.log2_bs));
       const bool bok = blk >= 0 && blk < a.ncb;
       const int row0 = ((bok ? blk : 0) * a.hkv + kvh) * a.bs + (base & (a.bs - 1));
       const bool kin = base + r < t1;
@@ -392,38 +372,6 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_part(DecodeArgs a) {
 // Every (dim, head) accumulator lives in exactly one lane, and a lane only ever rescales
 // its own head, so the running max/sum need no cross-lane traffic except on a rescale.
 
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-
-template <int DT> struct MfmaOps;
-template <> struct MfmaOps<MIP_BF16> {
-  static __device__ __forceinline__ f32x4_t qk(uint4 a, uint4 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                   c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4_t pv(uint2 a, uint2 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b),
-                                                     c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint16_t round16(float x) { return f32_to_bf16_rne(x); }
-  static __device__ __forceinline__ float widen16(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
-};
-template <> struct MfmaOps<MIP_F16> {
-  static __device__ __forceinline__ f32x4_t qk(uint4 a, uint4 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
-                                                  0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4_t pv(uint2 a, uint2 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c,
-                                                 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint16_t round16(float x) { return f32_to_f16_rne(x); }
-  static __device__ __forceinline__ float widen16(uint16_t h) { return f16_bits_to_f32(h); }
-};
-
 template <int D>
 struct MShape {
   static constexpr int KC = D / 32;                 // 16-byte loads per lane per tile row, QK K-steps
@@ -465,7 +413,7 @@ __device__ __forceinline__ void mfma_load(MFrag<D>& f, const DecodeArgs& a, cons
 #pragma unroll
     for (int t = 0; t < MS::TPW; ++t) {
       const int tb = __builtin_amdgcn_readfirstlane(base + 16 * t < t1 ? base + 16 * t : base);
-      const int blk = __builtin_amdgcn_readfirstlane(table[tb >> a.log2_bs]);
+      const int blk = load_uniform_i32(table + (tb >> a.log2_bs));
       const bool bok = blk >= 0 && blk < a.ncb;
       const int tok = base + 16 * t + i16;
       const bool in = tok < t1;
@@ -696,26 +644,29 @@ __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
 
 inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
-enum class Algo { kValu, kMfma };
+enum class Algo { kValu, kMfma, kStream };
 
 bool mfma_eligible(int dtype, int d, int g) {
   return (dtype == MIP_BF16 || dtype == MIP_F16) && (d == 64 || d == 128) && g >= 1 && g <= 16;
 }
 
-// MFMA for 16-bit data at head_dim 64/128 (the faster kernel under rocprof at the Qwen
-// shapes); the VALU kernel covers fp32 and the other head sizes. MIP_DECODE_ALGO=valu|mfma
-// forces one of them (diagnostics and the kernel comparison).
-Algo choose_algo(int dtype, int d, int g) {
+// Default: the stream-K MFMA kernel for 16-bit data at head_dim 64/128 (balanced persistent
+// work split, the fastest under rocprof at the Qwen shapes); the per-partition MFMA kernel
+// above kStreamMaxBatch; the VALU kernel for fp32 and the other head sizes.
+// MIP_DECODE_ALGO=valu|mfma|stream forces one where it applies (kernel comparison).
+Algo choose_algo(int dtype, int d, int g, int batch) {
   const char* env = std::getenv("MIP_DECODE_ALGO");
-  const int forced = !env ? 0 : env[0] == 'v' ? 1 : env[0] == 'm' ? 2 : 0;
+  const char f = env ? env[0] : 0;
   const bool mfma_ok = mfma_eligible(dtype, d, g);
-  if (forced == 1 && g <= 8) return Algo::kValu;
-  if (forced == 2 && mfma_ok) return Algo::kMfma;
-  return mfma_ok ? Algo::kMfma : Algo::kValu;
+  const bool stream_ok = mfma_ok && stream_config(dtype, d, g, batch).ok;
+  if (f == 'v' && g <= 8) return Algo::kValu;
+  if (f == 'm' && mfma_ok) return Algo::kMfma;
+  if (f == 's' && stream_ok) return Algo::kStream;
+  return stream_ok ? Algo::kStream : mfma_ok ? Algo::kMfma : Algo::kValu;
 }
 
 int pass_tokens(Algo algo, int dtype, int d) {
-  if (algo == Algo::kMfma) return d <= 64 ? 32 : 16;
+  if (algo != Algo::kValu) return d <= 64 ? 32 : 16;
   const int es = dtype == MIP_F32 ? 4 : 2;
   const int ch = d < 32 / es ? d : 32 / es;
   return kWave / (d / ch);
@@ -736,11 +687,25 @@ struct WsLayout {
   int part_tokens;
   int nparts;
   int64_t ml_off, acc_off, bytes;
+  StreamConfig stream;          // stream kernel launch shape
+  int64_t prefix_off, rec_off;  // stream kernel workspace
 };
 
 WsLayout ws_layout(int batch, int hq, int hkv, int d, int bs, int max_blocks, int dtype) {
   WsLayout w{};
-  w.algo = choose_algo(dtype, d, hq / hkv);
+  w.algo = choose_algo(dtype, d, hq / hkv, batch);
+  if (w.algo == Algo::kStream) {
+    w.stream = stream_config(dtype, d, hq / hkv, batch);
+    if (!w.stream.ok) {
+      w.algo = Algo::kMfma;
+    } else {
+      w.prefix_off = 0;
+      w.rec_off = align_up(static_cast<int64_t>(batch + 1) * 4, 256);
+      w.bytes = w.rec_off + align_up(static_cast<int64_t>(w.stream.tw) * 2 * w.stream.rec_floats * 4, 256);
+      w.nparts = 1;
+      return w;
+    }
+  }
   w.part_tokens = part_tokens_for(w.algo, dtype, d);
   const int64_t max_ctx = static_cast<int64_t>(max_blocks) * bs;
   w.nparts = static_cast<int>((max_ctx + w.part_tokens - 1) / w.part_tokens);
@@ -876,26 +841,29 @@ extern "C" int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_str
   if (!std::isfinite(scale)) return MIP_EINVAL;
   const int group = num_heads / num_kv_heads;
   const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
-  const KernelPair kp = pick_kernel(wl.algo, dtype, head_dim, group);
+  const KernelPair kp = pick_kernel(wl.algo == Algo::kStream ? Algo::kMfma : wl.algo, dtype, head_dim, group);
   if (!kp.part) return MIP_EUNSUPPORTED;
   const int64_t es = dtype == MIP_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return MIP_EINVAL;
-  const uint64_t q_align = wl.algo == Algo::kMfma ? 15 : 3;  // MFMA reads q rows with 16-byte loads
+  const uint64_t q_align = wl.algo == Algo::kValu ? 3 : 15;  // MFMA kernels read q rows with 16-byte loads
   if ((reinterpret_cast<uintptr_t>(q) | static_cast<uint64_t>(q_stride_b * es) |
        static_cast<uint64_t>(q_stride_h * es)) & q_align)
     return MIP_EINVAL;
+  const uint64_t out_align = wl.algo == Algo::kStream ? 7 : es - 1;  // the stream kernel stores 4 outputs at once
   if ((reinterpret_cast<uintptr_t>(out) | static_cast<uint64_t>(out_stride_b * es) |
-       static_cast<uint64_t>(out_stride_h * es)) & (es - 1))
+       static_cast<uint64_t>(out_stride_h * es)) & out_align)
     return MIP_EINVAL;
 
   DecodeArgs a{};
-  if (wl.nparts > 1) {
+  if (wl.nparts > 1 || wl.algo == Algo::kStream) {
     if (!workspace || workspace_bytes < static_cast<size_t>(wl.bytes) ||
         (reinterpret_cast<uintptr_t>(workspace) & 255))
       return MIP_EINVAL;
     char* ws = static_cast<char*>(workspace);
-    a.ws_ml = reinterpret_cast<float*>(ws + wl.ml_off);
-    a.ws_acc = reinterpret_cast<float*>(ws + wl.acc_off);
+    if (wl.algo != Algo::kStream) {
+      a.ws_ml = reinterpret_cast<float*>(ws + wl.ml_off);
+      a.ws_acc = reinterpret_cast<float*>(ws + wl.acc_off);
+    }
   }
   a.out = static_cast<char*>(out);
   a.out_sb = out_stride_b;
@@ -919,6 +887,16 @@ extern "C" int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_str
   a.scale_log2 = scale * 1.4426950408889634f;
   if (batch > 65535) return MIP_EINVAL;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (wl.algo == Algo::kStream) {
+    StreamArgs sa{};
+    sa.a = a;
+    sa.batch = batch;
+    sa.group = group;
+    sa.ws_prefix = reinterpret_cast<int*>(static_cast<char*>(workspace) + wl.prefix_off);
+    sa.ws_rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.rec_off);
+    const int st = stream_launch(wl.stream, sa, dtype, head_dim, group, num_kv_heads, batch, s);
+    return st == 0 ? MIP_OK : st;
+  }
   hipLaunchKernelGGL(kp.part, dim3(wl.nparts, num_kv_heads, batch), dim3(kNW * kWave), 0, s, a);
   if (wl.nparts > 1) hipLaunchKernelGGL(kp.merge, dim3(num_kv_heads, batch), dim3(256), 0, s, a);
   return status_from_hip(hipGetLastError());

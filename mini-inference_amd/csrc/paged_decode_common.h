@@ -1,0 +1,129 @@
+// Definitions shared by the paged decode-attention kernels (partition and stream-K).
+#pragma once
+
+#include <cmath>
+
+#include "mip_common.h"
+
+namespace mip {
+namespace decode {
+
+constexpr int kNW = 4;                  // wavefronts per workgroup
+constexpr float kRescaleLog2 = 8.0f;    // lazy-rescale threshold, log2 units (p <= 256)
+
+struct DecodeArgs {
+  char* out;
+  int64_t out_sb, out_sh;  // elements
+  const char* q;
+  int64_t q_sb, q_sh;      // elements
+  const char* k;
+  const char* v;
+  int64_t ncb;
+  const int32_t* bt;
+  int64_t bt_stride;
+  const int32_t* lens;
+  int hq, hkv, bs, log2_bs, max_blocks;
+  int part_tokens;
+  int nparts;
+  float scale_log2;
+  float* ws_acc;  // [B][Hq][nparts][D]
+  float* ws_ml;   // [B][Hq][nparts][2]
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v_t __attribute__((ext_vector_type(2)));
+
+template <int DT> struct MfmaOps;
+template <> struct MfmaOps<MIP_BF16> {
+  static __device__ __forceinline__ f32x4_t qk(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t pv(uint2 a, uint2 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b),
+                                                     c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t round16(float x) { return f32_to_bf16_rne(x); }
+  static __device__ __forceinline__ float widen16(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+  // Two floats -> packed pair (x in the low half), round to nearest even (v_cvt_pk_bf16_f32).
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{x, y}), bf16x2v_t));
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+};
+template <> struct MfmaOps<MIP_F16> {
+  static __device__ __forceinline__ f32x4_t qk(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t pv(uint2 a, uint2 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c,
+                                                 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t round16(float x) { return f32_to_f16_rne(x); }
+  static __device__ __forceinline__ float widen16(uint16_t h) { return f16_bits_to_f32(h); }
+  // Two floats -> packed pair (x in the low half), round to nearest even (v_cvt_pk_f16_f32).
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{x, y}), f16x2v_t));
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) { return f16_bits_to_f32(w & 0xffffu); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return f16_bits_to_f32(w >> 16); }
+};
+
+struct StreamArgs {
+  DecodeArgs a;
+  int batch;
+  int group;
+  int tw;          // wavefronts in the grid
+  int min_tiles;   // fewest tiles an active wavefront takes
+  int* ws_prefix;  // [batch + 1] tile prefix over sequences (written by workgroup 0)
+  float* ws_rec;   // [tw][2][rec_floats]
+};
+
+template <int D>
+struct SShape {
+  static constexpr int KC = D / 32;
+  static constexpr int MT = D / 16;
+  static constexpr int TILE_BYTES = 16 * D * 2;
+  static constexpr int REC = 32 + 16 * D;  // m[16], l[16], acc[16][D]
+};
+
+__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int stream_active_waves(int tw, int total_tiles, int min_tiles) {
+  const int want = (total_tiles + min_tiles - 1) / min_tiles;
+  const int w = want < tw ? want : tw;
+  return w > 0 ? w : 1;
+}
+
+// Launch the stream-K kernel and its merge (paged_decode_stream.hip). grid = workgroups;
+// returns 0 or a hipError_t.
+struct StreamConfig {
+  bool ok;          // a stream kernel exists for this (dtype, head_dim, group)
+  int grid;         // workgroups of the persistent grid (device capacity)
+  int tw;           // wavefronts in the grid
+  int lds_bytes;    // dynamic LDS per workgroup
+  int64_t rec_floats;
+};
+StreamConfig stream_config(int dtype, int d, int group, int batch);
+int stream_launch(const StreamConfig& cfg, const StreamArgs& sa, int dtype, int d, int group, int num_kv_heads,
+                  int batch, hipStream_t stream);
+
+}  // namespace decode
+}  // namespace mip

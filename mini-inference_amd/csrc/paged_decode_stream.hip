@@ -1,0 +1,580 @@
+// Stream-K paged decode attention for gfx950: persistent wavefronts, LDS ring fed by direct
+// global->LDS loads, MFMA tiles.
+//
+// Reference semantics: as paged_decode.hip (engine/kv_cache.py:615-620 gather + mask,
+// engine/model.py:126-147 GQA decode attention).
+//
+// Work split (16-bit K/V, head_dim 64/128, up to 16 query heads per kv head):
+//   * The grid is the device's resident capacity, so it is fixed and graph-capturable.
+//     Every workgroup copies the clamped context lengths into LDS and scans the per-sequence
+//     tile counts (16 keys per tile). Segment (sequence b, kv head) owns tiles
+//     [Hkv*P[b] + kvh*n_b, + n_b) of one global tile sequence of T tiles.
+//   * Wavefront gw streams tiles [gw*T/W, (gw+1)*T/W): equal shares regardless of how
+//     context lengths are distributed, crossing segment boundaries without a pause.
+//   * A segment a wavefront covers completely is normalised and written directly. A split
+//     segment leaves one record (m, l, unnormalised acc of 16 heads) per piece: slot 0 for
+//     the piece holding the wavefront's first tile, slot 1 for its last. The merge kernel
+//     combines the pieces.
+//
+// Memory pipeline (per wavefront, NS stages of K tile | V tile | q block in LDS):
+//   * global_load_lds_dwordx4 moves 64 x 16 bytes per instruction straight into LDS, so the
+//     loads in flight cost no registers. Stage i+NS-1 is issued before stage i is consumed.
+//   * The loop reads the ring only through inline-asm ds_read, after an explicit
+//     s_waitcnt vmcnt((NS-1) * loads-per-stage): the compiler cannot tell which ring stage a
+//     direct load fills and would otherwise drain every load before each LDS read. Block
+//     tables and context lengths are read with scalar loads, and cross-lane sums use
+//     v_permlane{16,32}_swap, so nothing else in the loop touches LDS.
+//   * K and q rows are stored with their 16-byte chunks XOR-swizzled by row, so the 16 rows
+//     read by one ds_read_b128 hit distinct banks. V is stored plainly; its transposed reads
+//     (ds_read_u16, one key per read, packed in pairs after the wait) have at most 4-way
+//     conflicts.
+//
+// Tile arithmetic (lane l: row/head l%16, lane group l/16):
+//   S^T[16 keys x 16 heads] = K . Q^T        v_mfma_f32_16x16x32_{bf16,f16}, D/32 steps
+//   O^T[D x 16 heads]      += V^T . P^T      v_mfma_f32_16x16x16_{bf16,f16}, D/16 M-tiles,
+//   P^T is the S^T output layout (kept in registers), split into hi + lo 16-bit parts so the
+//   PV product keeps ~fp32 precision. Online softmax in base 2 with a per-head running max
+//   that is only raised when a key exceeds it by more than kRescaleLog2.
+#include <cstdlib>
+#include <type_traits>
+
+#include "paged_decode_common.h"
+
+namespace mip {
+namespace decode {
+namespace {
+
+#ifndef MIP_STREAM_WAVES
+#define MIP_STREAM_WAVES 2
+#endif
+#ifndef MIP_STREAM_STAGES_D64
+#define MIP_STREAM_STAGES_D64 3
+#endif
+#ifndef MIP_STREAM_STAGES_D128
+#define MIP_STREAM_STAGES_D128 2
+#endif
+constexpr int kSW = MIP_STREAM_WAVES;   // wavefronts per workgroup
+constexpr int kStreamMaxBatch = 4096;   // context lengths + tile prefix fit in LDS
+
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) void gvoid_t;
+typedef __attribute__((address_space(3))) void lvoid_t;
+typedef __attribute__((address_space(3))) char lchar_t;
+
+template <int D, int QR>
+struct Ring {
+  static constexpr int RB = D * 2;              // bytes per key / value / query row
+  static constexpr int CPR = RB / 16;           // 16-byte chunks per row
+  static constexpr int RPD = 1024 / RB;         // rows per direct load (64 lanes x 16 bytes)
+  static constexpr int KI = 16 * RB / 1024;     // direct loads per 16-row K (or V) tile
+  static constexpr int QI = QR * RB / 1024;     // direct loads per q block of QR heads
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = 16 * RB;
+  static constexpr int Q_OFF = 32 * RB;
+  static constexpr int STAGE = (32 + QR) * RB;
+  static constexpr int DMA = 2 * KI + QI;       // direct loads per stage (static)
+  static constexpr int KC = D / 32;
+  static constexpr int MT = D / 16;
+  static_assert(QI >= 1, "q block must fill at least one direct load");
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+  // gfx9 s_waitcnt: vmcnt [3:0] and [15:14], expcnt [6:4] (7 = no wait), lgkmcnt [11:8] (15 = no wait).
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void dma16(const char* g, lchar_t* l) {
+  __builtin_amdgcn_global_load_lds((gvoid_t*)g, (lvoid_t*)l, 16, 0, 0);
+}
+
+template <int OFF>
+__device__ __forceinline__ u32x4_t lds_b128(uint32_t addr) {
+  u32x4_t r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+// Zero-extending 16-bit read into its own register. (The d16 / d16_hi forms that fill half a
+// register keep the other half as it was when the read was issued, so two of them in flight
+// to one register lose the first; the halves are packed after the wait instead.)
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_u16(uint32_t addr) {
+  uint32_t r;
+  asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+// Wait for the asm LDS reads, then pass each destination through an empty asm so every use
+// of it is ordered after the wait.
+__device__ __forceinline__ void lgkm_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void after_wait(u32x4_t& r) { asm volatile("" : "+v"(r)); }
+__device__ __forceinline__ void after_wait(uint32_t& r) { asm volatile("" : "+v"(r)); }
+
+// Sum / max over the four lanes l, l^16, l^32, l^48 with VALU lane swaps.
+__device__ __forceinline__ float sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float max4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+template <int V>
+using ic = std::integral_constant<int, V>;
+
+// Call f(ic<I>{}) for I = B .. E-1 (compile-time loop, for immediates such as LDS offsets).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(ic<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Call f(ic<I>{}) for I = B .. E-1 in order until one returns false; returns whether all did.
+template <int B, int E, typename F>
+__device__ __forceinline__ bool static_all(F&& f) {
+  if constexpr (B < E) {
+    if (!f(ic<B>{})) return false;
+    return static_all<B + 1, E>(f);
+  }
+  return true;
+}
+
+template <int DT, int D, int QR, int NS>
+__global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa) {
+  using R = Ring<D, QR>;
+  using Ops = MfmaOps<DT>;
+  using S = typename Elem<DT>::S;
+  constexpr int KC = R::KC, MT = R::MT, RB = R::RB, CPR = R::CPR, RPD = R::RPD;
+  constexpr int RING = NS * R::STAGE;
+  const DecodeArgs& a = sa.a;
+  const int B = sa.batch, G = sa.group;
+  extern __shared__ __attribute__((aligned(16))) char dsm[];
+  int* s_len = reinterpret_cast<int*>(dsm);  // [B] clamped context lengths
+  int* s_pre = s_len + B;                     // [B + 1] exclusive tile prefix over sequences
+  int* s_wtot = s_pre + B + 1;                // [kSW] per-wavefront scan totals
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int i16 = lane & 15, grp = lane >> 4;
+  const int cap = a.max_blocks * a.bs;
+
+  // ---- work split: context lengths -> tile prefix (block-wide exclusive scan).
+  for (int i = tid; i < B; i += kSW * kWave) {
+    int L = a.lens[i];
+    L = L < cap ? L : cap;
+    s_len[i] = L > 0 ? L : 0;
+  }
+  __syncthreads();
+  {
+    const int chunk = (B + kSW * kWave - 1) / (kSW * kWave);
+    const int beg = tid * chunk < B ? tid * chunk : B;
+    const int end = beg + chunk < B ? beg + chunk : B;
+    int sum = 0;
+    for (int i = beg; i < end; ++i) sum += (s_len[i] + 15) >> 4;
+    const int incl = wave_inclusive_scan(sum, lane);
+    if (lane == kWave - 1) s_wtot[w] = incl;
+    __syncthreads();
+    int off = 0;
+    for (int j = 0; j < w; ++j) off += s_wtot[j];
+    int run = off + incl - sum;
+    for (int i = beg; i < end; ++i) {
+      s_pre[i] = run;
+      run += (s_len[i] + 15) >> 4;
+    }
+    if (tid == kSW * kWave - 1) s_pre[B] = off + incl;
+  }
+  __syncthreads();
+  const int total = a.hkv * s_pre[B];
+  if (blockIdx.x == 0) {
+    for (int i = tid; i <= B; i += kSW * kWave) sa.ws_prefix[i] = s_pre[i];
+  }
+  const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
+  const int gw = blockIdx.x * kSW + w;
+  const bool active = total > 0 && gw < tw;
+  int lo = 0, hi = 0, cb = 0, ckvh = 0, ct = 0;
+  if (active) {
+    lo = static_cast<int>(static_cast<int64_t>(gw) * total / tw);
+    hi = static_cast<int>(static_cast<int64_t>(gw + 1) * total / tw);
+    int lb = 0, ub = B - 1;  // largest b with Hkv * P[b] <= lo; its segment is not empty
+    while (lb < ub) {
+      const int mid = (lb + ub + 1) >> 1;
+      if (a.hkv * __builtin_amdgcn_readfirstlane(s_pre[mid]) <= lo) lb = mid; else ub = mid - 1;
+    }
+    cb = lb;
+    const int n = __builtin_amdgcn_readfirstlane((s_len[cb] + 15) >> 4);
+    const int rem = lo - a.hkv * __builtin_amdgcn_readfirstlane(s_pre[cb]);
+    ckvh = rem / n;
+    ct = rem - ckvh * n;
+  }
+  __syncthreads();  // the rings below reuse the scan area
+  if (!active || lo >= hi) return;
+
+  auto seq_len = [&](int b) __attribute__((always_inline)) {
+    int L = load_uniform_i32(a.lens + b);
+    L = L < cap ? L : cap;
+    return L > 0 ? L : 0;
+  };
+  int cL = seq_len(cb);
+  int cn = (cL + 15) >> 4;
+  int pb = cb, pkvh = ckvh, pt = ct, pL = cL, pn = cn;  // producer cursor (next tile to load)
+  auto advance = [&](int& b_, int& kvh_, int& t_, int& L_, int& n_) __attribute__((always_inline)) {
+    if (++t_ < n_) return;
+    t_ = 0;
+    if (++kvh_ < a.hkv) return;
+    kvh_ = 0;
+    do {
+      ++b_;
+      L_ = b_ < B ? seq_len(b_) : 16;
+      n_ = (L_ + 15) >> 4;
+    } while (n_ == 0);
+  };
+
+  // ---- per-lane LDS addresses (ring base of this wavefront; stage offsets are immediates).
+  lchar_t* lds = (lchar_t*)(dsm);  // address-space cast: generic -> LDS
+  lchar_t* ring_ptr = lds + w * RING;
+  const uint32_t ring = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring_ptr));
+  uint32_t k_addr[KC], q_addr[KC];
+  const int qrow = i16 & (QR - 1);
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    const int c = 4 * kc + grp;
+    k_addr[kc] = ring + R::K_OFF + i16 * RB + ((c ^ (i16 & (CPR - 1))) * 16);
+    q_addr[kc] = ring + R::Q_OFF + qrow * RB + ((c ^ (qrow & (CPR - 1))) * 16);
+  }
+  const uint32_t v_addr = ring + R::V_OFF + (4 * grp) * RB + i16 * 2;
+  const int dma_r = lane / CPR, dma_pc = lane % CPR;
+
+  uint32_t vmask[NS];  // per stage: bit r = key row r of the tile is a key of its segment
+
+  auto produce = [&](auto stage_c, auto scalar_table) __attribute__((always_inline)) {
+    constexpr int s = decltype(stage_c)::value;
+    lchar_t* st = ring_ptr + s * R::STAGE;
+    const int tb = 16 * pt;
+    const int32_t* table = a.bt + static_cast<int64_t>(pb) * a.bt_stride;
+    if constexpr (decltype(scalar_table)::value) {
+      // block_size >= 16: the tile lies in one block.
+      const int blk = load_uniform_i32(table + (tb >> a.log2_bs));
+      const bool bok = blk >= 0 && blk < a.ncb;
+      const int rem = pL - tb;
+      const int nvalid = bok ? (rem < 16 ? rem : 16) : 0;
+      vmask[s] = nvalid >= 16 ? 0xffffu : ((1u << nvalid) - 1u);
+      const int64_t row0 = static_cast<int64_t>((bok ? blk : 0) * a.hkv + pkvh) * a.bs + (tb & (a.bs - 1));
+#pragma unroll
+      for (int j = 0; j < R::KI; ++j) {
+        const int r = j * RPD + dma_r;
+        const int64_t row = row0 + (r < nvalid ? r : 0);
+        const int lc = dma_pc ^ (r & (CPR - 1));
+        dma16(a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
+        dma16(a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
+      }
+    } else {
+      // Small blocks: every row looks its block up; rows that are not keys re-read the
+      // tile's first key (block 0 if even that id is out of range, which the mask drops).
+      const int tk0 = tb;
+      const int b0 = table[tk0 >> a.log2_bs];
+      const bool ok0 = b0 >= 0 && b0 < a.ncb;
+      const int64_t row_first = static_cast<int64_t>((ok0 ? b0 : 0) * a.hkv + pkvh) * a.bs + (tk0 & (a.bs - 1));
+      {
+        const int tok = tb + i16;
+        const int bl = table[(tok < pL ? tok : tk0) >> a.log2_bs];
+        const bool ok = tok < pL && bl >= 0 && bl < a.ncb;
+        vmask[s] = static_cast<uint32_t>(__ballot(ok)) & 0xffffu;
+      }
+#pragma unroll
+      for (int j = 0; j < R::KI; ++j) {
+        const int r = j * RPD + dma_r;
+        const int tok = tb + r;
+        const int bl = table[(tok < pL ? tok : tk0) >> a.log2_bs];
+        const bool ok = tok < pL && bl >= 0 && bl < a.ncb;
+        const int64_t row = ok ? static_cast<int64_t>(bl * a.hkv + pkvh) * a.bs + (tok & (a.bs - 1)) : row_first;
+        const int lc = dma_pc ^ (r & (CPR - 1));
+        dma16(a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
+        dma16(a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < R::QI; ++j) {
+      const int hr = j * RPD + dma_r;
+      const int hh = hr < G ? hr : 0;
+      const int lc = dma_pc ^ (hr & (CPR - 1));
+      dma16(a.q + (static_cast<int64_t>(pb) * a.q_sb + static_cast<int64_t>(pkvh * G + hh) * a.q_sh) * 2 + lc * 16,
+            st + R::Q_OFF + j * 1024);
+    }
+  };
+
+  f32x4_t acc[MT];
+  u32x4_t qreg[KC];
+  float m = -INFINITY, l = 0.0f;
+  bool full_start = false;  // the current segment started at its tile 0 in this wavefront
+  bool first_seg = true;    // the current segment holds this wavefront's first tile
+  const bool live = i16 < G;
+  S* out_base = reinterpret_cast<S*>(a.out);
+
+  auto consume = [&](auto stage_c, int i) __attribute__((always_inline)) {
+    constexpr int s = decltype(stage_c)::value;
+    constexpr int SO = s * R::STAGE;
+    wait_vmcnt<(NS - 1) * R::DMA>();
+    if (ct == 0 || i == lo) {
+      m = -INFINITY;
+      l = 0.0f;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      full_start = ct == 0;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) qreg[kc] = lds_b128<SO>(q_addr[kc]);
+      lgkm_wait();
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) after_wait(qreg[kc]);
+    }
+    const uint32_t vm = vmask[s];
+    u32x4_t kreg[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) kreg[kc] = lds_b128<SO>(k_addr[kc]);
+    uint32_t ve[MT][4];  // V^T operand halves: keys 4*grp + e at dim 16*mt + i16
+    if (vm) {
+      static_for<0, MT>([&](auto mtc) {
+        constexpr int mt = decltype(mtc)::value;
+        ve[mt][0] = lds_u16<SO + 0 * RB + 32 * mt>(v_addr);
+        ve[mt][1] = lds_u16<SO + 1 * RB + 32 * mt>(v_addr);
+        ve[mt][2] = lds_u16<SO + 2 * RB + 32 * mt>(v_addr);
+        ve[mt][3] = lds_u16<SO + 3 * RB + 32 * mt>(v_addr);
+      });
+    }
+    lgkm_wait();
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) after_wait(kreg[kc]);
+    uint32_t vt[MT][2];
+    if (vm) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) after_wait(ve[mt][e]);
+        vt[mt][0] = ve[mt][0] | (ve[mt][1] << 16);
+        vt[mt][1] = ve[mt][2] | (ve[mt][3] << 16);
+      }
+    }
+
+    f32x4_t st = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+      st = Ops::qk(__builtin_bit_cast(uint4, kreg[kc]), __builtin_bit_cast(uint4, qreg[kc]), st);
+    float sv[4];
+    bool need = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = live && ((vm >> (4 * grp + j)) & 1u);
+      sv[j] = ok ? st[j] * a.scale_log2 : -INFINITY;
+      need |= sv[j] > m + kRescaleLog2;
+    }
+    if (__any(need)) {
+      const float mx = max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+      const float mn = fmaxf(m, mx);
+      const float alpha = (m == -INFINITY) ? 0.0f : fast_exp2(m - mn);
+      l *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] *= alpha;
+      m = mn;
+    }
+    if (vm) {
+      // P as hi + lo 16-bit parts: p = hi + lo to ~2^-16 relative (bf16) or better (fp16).
+      uint32_t ph[2], pl[2];
+#pragma unroll
+      for (int j = 0; j < 4; j += 2) {
+        const float p0 = sv[j] == -INFINITY ? 0.0f : fast_exp2(sv[j] - m);
+        const float p1 = sv[j + 1] == -INFINITY ? 0.0f : fast_exp2(sv[j + 1] - m);
+        l += p0 + p1;
+        ph[j / 2] = Ops::pack2(p0, p1);
+        pl[j / 2] = Ops::pack2(p0 - Ops::lo(ph[j / 2]), p1 - Ops::hi(ph[j / 2]));
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint2 va = make_uint2(vt[mt][0], vt[mt][1]);
+        acc[mt] = Ops::pv(va, make_uint2(ph[0], ph[1]), acc[mt]);
+        acc[mt] = Ops::pv(va, make_uint2(pl[0], pl[1]), acc[mt]);
+      }
+    }
+
+    if (ct == cn - 1 || i == hi - 1) {
+      const float lt = sum4(l);
+      if (full_start && ct == cn - 1) {
+        if (live) {
+          const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+          S* orow = out_base + static_cast<int64_t>(cb) * a.out_sb + static_cast<int64_t>(ckvh * G + i16) * a.out_sh;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const uint32_t w0 = Ops::pack2(acc[mt][0] * inv, acc[mt][1] * inv);
+            const uint32_t w1 = Ops::pack2(acc[mt][2] * inv, acc[mt][3] * inv);
+            *reinterpret_cast<uint2*>(orow + 16 * mt + 4 * grp) = make_uint2(w0, w1);
+          }
+        }
+      } else {
+        float* rec = sa.ws_rec + (static_cast<int64_t>(gw) * 2 + (first_seg ? 0 : 1)) * SShape<D>::REC;
+        if (grp == 0) {
+          rec[i16] = m;
+          rec[16 + i16] = lt;
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          *reinterpret_cast<f32x4_t*>(rec + 32 + i16 * D + 16 * mt + 4 * grp) = acc[mt];
+      }
+      first_seg = false;
+    }
+  };
+
+  // The producer cursor moves to tile x only while x < hi; past the end it stays on the
+  // last tile, which is loaded again so every stage issues the same number of loads.
+  auto adv_p = [&](int x) __attribute__((always_inline)) {
+    if (x < hi) advance(pb, pkvh, pt, pL, pn);
+  };
+  auto run = [&](auto scalar_table) __attribute__((always_inline)) {
+    // Prologue: tiles lo .. lo+NS-2 into stages 0 .. NS-2.
+    static_for<0, NS - 1>([&](auto kc) __attribute__((always_inline)) {
+      constexpr int k = decltype(kc)::value;
+      if constexpr (k > 0) adv_p(lo + k);
+      produce(ic<k>{}, scalar_table);
+    });
+    int i = lo;
+    // Step on stage k: load tile i+NS-1 into the stage freed last step, then compute tile i.
+    auto step = [&](auto kc) __attribute__((always_inline)) -> bool {
+      constexpr int k = decltype(kc)::value;
+      adv_p(i + NS - 1);
+      produce(ic<(k + NS - 1) % NS>{}, scalar_table);
+      consume(ic<k>{}, i);
+      if (++i >= hi) return false;
+      advance(cb, ckvh, ct, cL, cn);
+      return true;
+    };
+    while (static_all<0, NS>(step)) {
+    }
+  };
+  if (a.bs >= 16) {
+    run(std::true_type{});
+  } else {
+    run(std::false_type{});
+  }
+  wait_vmcnt<0>();  // no direct load may land in LDS after this wavefront ends
+}
+
+// Combine the pieces of every segment the stream kernel split. Grid (kv heads, batch).
+template <int DT, int D>
+__global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) {
+  using S = typename Elem<DT>::S;
+  constexpr int REC = SShape<D>::REC;
+  const DecodeArgs& a = sa.a;
+  const int kvh = blockIdx.x, b = blockIdx.y, G = sa.group;
+  S* out_base = reinterpret_cast<S*>(a.out);
+  const int cap = a.max_blocks * a.bs;
+  int L = a.lens[b];
+  L = L < cap ? L : cap;
+  if (L <= 0) {
+    for (int i = threadIdx.x; i < G * D; i += blockDim.x)
+      out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + i / D) * a.out_sh + i % D] =
+          from_f32<DT>(0.0f);
+    return;
+  }
+  const int total = a.hkv * sa.ws_prefix[sa.batch];
+  const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
+  const int n = (L + 15) >> 4;
+  const int64_t s0 = static_cast<int64_t>(a.hkv) * sa.ws_prefix[b] + static_cast<int64_t>(kvh) * n;
+  const int64_t e1 = s0 + n - 1;
+  const int gw_lo = static_cast<int>(((s0 + 1) * tw - 1) / total);
+  const int gw_hi = static_cast<int>(((e1 + 1) * tw - 1) / total);
+  if (gw_lo == gw_hi) return;  // one wavefront held the whole segment and wrote it
+  const bool lo_split = static_cast<int64_t>(gw_lo) * total / tw < s0;
+  for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
+    const int g = i / D, d = i % D;
+    float mx = -INFINITY;
+    for (int gw = gw_lo; gw <= gw_hi; ++gw) {
+      const float* rec = sa.ws_rec + (static_cast<int64_t>(gw) * 2 + (gw == gw_lo && lo_split ? 1 : 0)) * REC;
+      mx = fmaxf(mx, rec[g]);
+    }
+    float A = 0.0f, Ls = 0.0f;
+    for (int gw = gw_lo; gw <= gw_hi; ++gw) {
+      const float* rec = sa.ws_rec + (static_cast<int64_t>(gw) * 2 + (gw == gw_lo && lo_split ? 1 : 0)) * REC;
+      const float mp = rec[g];
+      const float wt = (mp == -INFINITY) ? 0.0f : fast_exp2(mp - mx);
+      A = fmaf(wt, rec[32 + g * D + d], A);
+      Ls = fmaf(wt, rec[16 + g], Ls);
+    }
+    out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + g) * a.out_sh + d] =
+        from_f32<DT>(Ls > 0.0f ? A / Ls : 0.0f);
+  }
+}
+
+using StreamFn = void (*)(StreamArgs);
+
+struct StreamPick {
+  StreamFn main = nullptr;
+  StreamFn merge = nullptr;
+  int ring_bytes = 0;  // per wavefront
+};
+
+template <int DT, int D, int QR>
+StreamPick pick_one() {
+  constexpr int NS = D == 64 ? MIP_STREAM_STAGES_D64 : MIP_STREAM_STAGES_D128;
+  return {paged_decode_stream<DT, D, QR, NS>, paged_decode_stream_merge<DT, D>, NS * Ring<D, QR>::STAGE};
+}
+
+StreamPick pick(int dtype, int d, int group) {
+  const bool q8 = group <= 8;
+  if (dtype == MIP_BF16) {
+    if (d == 64) return q8 ? pick_one<MIP_BF16, 64, 8>() : pick_one<MIP_BF16, 64, 16>();
+    if (d == 128) return q8 ? pick_one<MIP_BF16, 128, 8>() : pick_one<MIP_BF16, 128, 16>();
+  } else if (dtype == MIP_F16) {
+    if (d == 64) return q8 ? pick_one<MIP_F16, 64, 8>() : pick_one<MIP_F16, 64, 16>();
+    if (d == 128) return q8 ? pick_one<MIP_F16, 128, 8>() : pick_one<MIP_F16, 128, 16>();
+  }
+  return {};
+}
+
+int stream_min_tiles() {
+  if (const char* env = std::getenv("MIP_STREAM_MIN_TILES")) {
+    const int v = std::atoi(env);
+    if (v > 0) return v;
+  }
+  return 4;
+}
+
+}  // namespace
+
+StreamConfig stream_config(int dtype, int d, int group, int batch) {
+  StreamConfig c{};
+  if (batch < 1 || batch > kStreamMaxBatch || group < 1 || group > 16) return c;
+  const StreamPick p = pick(dtype, d, group);
+  if (!p.main) return c;
+  const int scan_bytes = (2 * batch + 1 + kSW) * 4;
+  const int ring_bytes = kSW * p.ring_bytes;
+  c.lds_bytes = scan_bytes > ring_bytes ? scan_bytes : ring_bytes;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return c;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return c;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(p.main), kSW * kWave,
+                                                   c.lds_bytes) != hipSuccess)
+    return c;
+  c.grid = cus * (per_cu > 0 ? per_cu : 1);
+  c.tw = c.grid * kSW;
+  c.rec_floats = 32 + 16 * static_cast<int64_t>(d);
+  c.ok = true;
+  return c;
+}
+
+int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, int d, int group, int num_kv_heads,
+                  int batch, hipStream_t stream) {
+  const StreamPick p = pick(dtype, d, group);
+  StreamArgs sa = sa_in;
+  sa.tw = cfg.tw;
+  sa.min_tiles = stream_min_tiles();
+  hipLaunchKernelGGL(p.main, dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
+  hipLaunchKernelGGL(p.merge, dim3(num_kv_heads, batch), dim3(256), 0, stream, sa);
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace decode
+}  // namespace mip

@@ -207,7 +207,7 @@ def _check_decode(gpu, dtype, batch, hq, hkv, d, bs, lens, seed=0, stale=None, m
     return err
 
 
-@pytest.fixture(params=["default", "valu", "mfma"])
+@pytest.fixture(params=["default", "valu", "mfma", "stream"])
 def algo(request, monkeypatch):
     """Which partition kernel the library picks (MIP_DECODE_ALGO; ignored where a kernel does not apply)."""
     if request.param != "default":
