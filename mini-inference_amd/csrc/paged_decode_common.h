@@ -85,8 +85,9 @@ struct StreamArgs {
   int group;
   int tw;          // wavefronts in the grid
   int min_tiles;   // fewest tiles an active wavefront takes
+  int rec_stride;  // floats per record: m[16] | l[16] | acc[group][D]
   int* ws_prefix;  // [batch + 1] tile prefix over sequences (written by workgroup 0)
-  float* ws_rec;   // [tw][2][rec_floats]
+  float* ws_rec;   // [tw][2][rec_stride]
 };
 
 template <int D>
@@ -94,7 +95,6 @@ struct SShape {
   static constexpr int KC = D / 32;
   static constexpr int MT = D / 16;
   static constexpr int TILE_BYTES = 16 * D * 2;
-  static constexpr int REC = 32 + 16 * D;  // m[16], l[16], acc[16][D]
 };
 
 __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {

@@ -415,14 +415,16 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
           }
         }
       } else {
-        float* rec = sa.ws_rec + (static_cast<int64_t>(gw) * 2 + (first_seg ? 0 : 1)) * SShape<D>::REC;
-        if (grp == 0) {
-          rec[i16] = m;
-          rec[16 + i16] = lt;
-        }
+        float* rec = sa.ws_rec + (static_cast<int64_t>(gw) * 2 + (first_seg ? 0 : 1)) * sa.rec_stride;
+        if (live) {
+          if (grp == 0) {
+            rec[i16] = m;
+            rec[16 + i16] = lt;
+          }
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          *reinterpret_cast<f32x4_t*>(rec + 32 + i16 * D + 16 * mt + 4 * grp) = acc[mt];
+          for (int mt = 0; mt < MT; ++mt)
+            *reinterpret_cast<f32x4_t*>(rec + 32 + i16 * D + 16 * mt + 4 * grp) = acc[mt];
+        }
       }
       first_seg = false;
     }
@@ -466,7 +468,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
 template <int DT, int D>
 __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) {
   using S = typename Elem<DT>::S;
-  constexpr int REC = SShape<D>::REC;
+  const int64_t REC = sa.rec_stride;
   const DecodeArgs& a = sa.a;
   const int kvh = blockIdx.x, b = blockIdx.y, G = sa.group;
   S* out_base = reinterpret_cast<S*>(a.out);
@@ -488,23 +490,93 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
   const int gw_hi = static_cast<int>(((e1 + 1) * tw - 1) / total);
   if (gw_lo == gw_hi) return;  // one wavefront held the whole segment and wrote it
   const bool lo_split = static_cast<int64_t>(gw_lo) * total / tw < s0;
-  for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
-    const int g = i / D, d = i % D;
-    float mx = -INFINITY;
-    for (int gw = gw_lo; gw <= gw_hi; ++gw) {
-      const float* rec = sa.ws_rec + (static_cast<int64_t>(gw) * 2 + (gw == gw_lo && lo_split ? 1 : 0)) * REC;
-      mx = fmaxf(mx, rec[g]);
+  const int R = gw_hi - gw_lo + 1;
+  // Record r of this segment: the first piece sits in the "last segment" slot of wavefront
+  // gw_lo when that wavefront started inside an earlier segment, every other piece in the
+  // "first segment" slot of its wavefront.
+  auto rec_of = [&](int r) -> const float* {
+    return sa.ws_rec + (static_cast<int64_t>(gw_lo + r) * 2 + (r == 0 && lo_split ? 1 : 0)) * REC;
+  };
+  // One pass over chunks of 16 records with an online maximum per row. Every thread owns up
+  // to two quads of four output columns of one row; the quads' partial sums of a chunk are
+  // loaded together with the chunk's (m, l) pairs, so a chunk costs one memory round trip.
+  constexpr int kRC = 16;
+  constexpr int Q = D / 4;  // column quads per row
+  __shared__ float s_m[kRC][16];
+  __shared__ float s_l[kRC][16];
+  const int t = threadIdx.x, tg = t & 15, tr = t >> 4;
+  const int nq = G * Q;  // quads per (kv head, sequence): at most 512
+  const int nj = nq > 256 ? 2 : 1;
+  float4 acc[2];
+  float mrun[2], lrun[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    mrun[j] = -INFINITY;
+    lrun[j] = 0.0f;
+  }
+  for (int c0 = 0; c0 < R; c0 += kRC) {
+    const int nr = R - c0 < kRC ? R - c0 : kRC;
+    float4 v[2][kRC];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int qd = t + 256 * j;
+      if (j < nj && qd < nq) {
+        const int g = qd / Q, col = (qd % Q) * 4;
+#pragma unroll
+        for (int k = 0; k < kRC; ++k)
+          if (k < nr) v[j][k] = *reinterpret_cast<const float4*>(rec_of(c0 + k) + 32 + g * D + col);
+      }
     }
-    float A = 0.0f, Ls = 0.0f;
-    for (int gw = gw_lo; gw <= gw_hi; ++gw) {
-      const float* rec = sa.ws_rec + (static_cast<int64_t>(gw) * 2 + (gw == gw_lo && lo_split ? 1 : 0)) * REC;
-      const float mp = rec[g];
-      const float wt = (mp == -INFINITY) ? 0.0f : fast_exp2(mp - mx);
-      A = fmaf(wt, rec[32 + g * D + d], A);
-      Ls = fmaf(wt, rec[16 + g], Ls);
+    float mp = -INFINITY, lp = 0.0f;
+    if (tg < G && tr < nr) {
+      const float* rec = rec_of(c0 + tr);
+      mp = rec[tg];
+      lp = rec[16 + tg];
     }
-    out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + g) * a.out_sh + d] =
-        from_f32<DT>(Ls > 0.0f ? A / Ls : 0.0f);
+    s_m[tr][tg] = mp;
+    s_l[tr][tg] = lp;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int qd = t + 256 * j;
+      if (j < nj && qd < nq) {
+        const int g = qd / Q;
+        float cm = mrun[j];
+        for (int k = 0; k < nr; ++k) cm = fmaxf(cm, s_m[k][g]);
+        const float alpha = mrun[j] == -INFINITY ? 0.0f : fast_exp2(mrun[j] - cm);
+        float4 s = make_float4(acc[j].x * alpha, acc[j].y * alpha, acc[j].z * alpha, acc[j].w * alpha);
+        float ls = lrun[j] * alpha;
+#pragma unroll
+        for (int k = 0; k < kRC; ++k)
+          if (k < nr) {
+            const float mk = s_m[k][g];
+            const float wk = mk == -INFINITY ? 0.0f : fast_exp2(mk - cm);
+            s.x = fmaf(wk, v[j][k].x, s.x);
+            s.y = fmaf(wk, v[j][k].y, s.y);
+            s.z = fmaf(wk, v[j][k].z, s.z);
+            s.w = fmaf(wk, v[j][k].w, s.w);
+            ls = fmaf(wk, s_l[k][g], ls);
+          }
+        acc[j] = s;
+        lrun[j] = ls;
+        mrun[j] = cm;
+      }
+    }
+    __syncthreads();  // the next chunk overwrites s_m / s_l
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int qd = t + 256 * j;
+    if (j < nj && qd < nq) {
+      const int g = qd / Q, col = (qd % Q) * 4;
+      const float inv = lrun[j] > 0.0f ? 1.0f / lrun[j] : 0.0f;
+      S* o = out_base + static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + g) * a.out_sh + col;
+      o[0] = from_f32<DT>(acc[j].x * inv);
+      o[1] = from_f32<DT>(acc[j].y * inv);
+      o[2] = from_f32<DT>(acc[j].z * inv);
+      o[3] = from_f32<DT>(acc[j].w * inv);
+    }
   }
 }
 
@@ -560,7 +632,7 @@ StreamConfig stream_config(int dtype, int d, int group, int batch) {
     return c;
   c.grid = cus * (per_cu > 0 ? per_cu : 1);
   c.tw = c.grid * kSW;
-  c.rec_floats = 32 + 16 * static_cast<int64_t>(d);
+  c.rec_floats = 32 + static_cast<int64_t>(group) * d;
   c.ok = true;
   return c;
 }
@@ -571,6 +643,7 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, i
   StreamArgs sa = sa_in;
   sa.tw = cfg.tw;
   sa.min_tiles = stream_min_tiles();
+  sa.rec_stride = static_cast<int>(cfg.rec_floats);
   hipLaunchKernelGGL(p.main, dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
   hipLaunchKernelGGL(p.merge, dim3(num_kv_heads, batch), dim3(256), 0, stream, sa);
   return static_cast<int>(hipGetLastError());
