@@ -9,10 +9,11 @@ are resident in HBM before the timed region; the pool holds N(0, 1) data.
 
 Reported (one JSON line on stdout):
   value         algorithmic bytes of the step (append + attention, 24 layers) / step time, GB/s
-  roofline      the paged decode-attention kernel alone: algorithmic bytes per launch /
-                average launch duration (HIP events over a timed loop of its launches),
-                against the 8 TB/s HBM peak; traffic = measured HBM bytes per launch when a
-                counter summary exists under profiles/
+  roofline      one paged decode-attention call (the stream kernel paged_decode_stream plus
+                its partition merge paged_decode_stream_merge, launched back to back on the
+                caller's stream): algorithmic bytes per call / average call duration (HIP events
+                around a timed loop of the calls), against the 8 TB/s HBM peak; traffic = measured
+                HBM bytes per call when a counter summary exists under profiles/
   decode_tok_s  B / full decode-step time of a random-init Qwen2.5-0.5B (embedding, 24 layers
                 with GEMMs, RoPE, append, attention, MLP, final norm, logits)
   cpu_baseline  the reference's torch CPU path (index_put_ append + table gather + SDPA,
@@ -41,7 +42,7 @@ for _p in (ROOT, ROOT / "mini-inference_amd"):
 
 HBM_PEAK_GBPS = 8000.0
 METRIC = "paged decode-attn HBM GB/s (% of peak) + decode tok/s, Qwen2.5-0.5B b256"
-TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_bf16_b256_ctx128-4096_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_stream_bf16_b256_ctx128-4096_traffic.json"
 
 
 def log(msg: str) -> None:
@@ -156,6 +157,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (about)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-model", action="store_true", help="skip the full-model decode tok/s measurement")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 512 MiB device copy three times (HBM counter scale for rocprofv3 --pmc)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -172,6 +175,13 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda", 0)
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.bfloat16, device=dev)  # 512 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     shape = workloads.SHAPES[3]
     t0 = time.perf_counter()
     batch = workloads.build_decode_batch(shape, dev, seed=0)
@@ -251,7 +261,7 @@ def main() -> int:
         "frac_of_peak": round(value / HBM_PEAK_GBPS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_valu<bf16, D=64, G=7>",
+            "kernel": "paged_decode_stream<bf16, D=64, QR=8, NS=3> + paged_decode_stream_merge<bf16, D=64>",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
