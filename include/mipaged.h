@@ -94,11 +94,12 @@ int mip_kv_append(const void* k_src, const void* v_src,
  * context_lens[b] must not exceed max_blocks_per_seq * block_size (larger values are
  * clamped to it).
  *
- * `workspace` must hold mip_paged_decode_workspace(...) bytes for the same shape, be
- * 256-byte aligned and be zero-filled ONCE when first allocated: the kernel leaves its
- * counters at zero again when it finishes, so the buffer can be reused by later calls
- * on the same stream without clearing. Two calls that run concurrently must not share
- * a workspace.
+ * `workspace` is scratch device memory for split contexts (per-piece softmax state and
+ * partial outputs, combined by a second kernel on the same stream). It must hold
+ * mip_paged_decode_workspace(...) bytes for the same shape, asked with the same device
+ * current, and be 256-byte aligned. It needs no initialisation and its contents are
+ * undefined afterwards; calls on one stream may reuse it, calls that can run
+ * concurrently must not share it.
  */
 int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h,
                      const void* q, int64_t q_stride_b, int64_t q_stride_h,

@@ -651,8 +651,9 @@ bool mfma_eligible(int dtype, int d, int g) {
 }
 
 // Default: the stream-K MFMA kernel for 16-bit data at head_dim 64/128 (balanced persistent
-// work split, the fastest under rocprof at the Qwen shapes); the per-partition MFMA kernel
-// above kStreamMaxBatch; the VALU kernel for fp32 and the other head sizes.
+// work split, the fastest under rocprof at the Qwen shapes) while its per-sequence scan fits
+// in LDS (batch <= 4096); otherwise the per-partition MFMA kernel; the VALU kernel for fp32
+// and the other head sizes.
 // MIP_DECODE_ALGO=valu|mfma|stream forces one where it applies (kernel comparison).
 Algo choose_algo(int dtype, int d, int g, int batch) {
   const char* env = std::getenv("MIP_DECODE_ALGO");

@@ -99,13 +99,12 @@ def kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: 
 
 
 class _Workspace:
-    """One zero-initialised scratch buffer per device, grown on demand.
+    """One scratch buffer per device, grown on demand (no initialisation needed).
 
-    The decode kernel leaves its counters at zero when it finishes, so the buffer is
-    zero-filled only when it is (re)allocated. Calls that use it must be ordered (one
-    stream, or graph replays on that stream): two decode calls running concurrently on
-    different streams of one device would race on it; pass ``workspace=`` to each instead.
-    Allocate it before graph capture (one eager call with the largest shape).
+    Calls that use it must be ordered (one stream, or graph replays on that stream): two
+    decode calls running concurrently on different streams of one device would race on
+    it; pass ``workspace=`` to each instead. Allocate it before graph capture (one eager
+    call with the largest shape).
     """
 
     def __init__(self) -> None:
@@ -118,7 +117,7 @@ class _Workspace:
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
             size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
             self._bufs[key] = buf
         return buf
 

@@ -61,7 +61,9 @@ def f16_to_f32(bits: np.ndarray) -> np.ndarray:
 
 
 def f32_to_f16(x: np.ndarray) -> np.ndarray:
-    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+    """float32 -> float16 bit patterns, round to nearest even; values beyond 65504 round to inf."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
 
 
 def widen(a: np.ndarray, dtype: str) -> np.ndarray:

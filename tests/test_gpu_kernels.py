@@ -273,6 +273,35 @@ def test_paged_decode_config1_golden(gpu):
     assert np.abs(values(got) - want_t.numpy()).max() < 2e-5
 
 
+def test_paged_decode_golden_fixture(gpu):
+    """The committed golden case (tests/golden): append + attention through the C ABI vs the fixture."""
+    import json
+
+    import cfg1
+    from engine import paged_ops
+
+    announce("golden fixture cfg1 fp32 decode step")
+    meta = json.loads(cfg1.META.read_text())
+    gold = np.load(cfg1.NPZ)
+    inp = cfg1.make_inputs()
+    assert cfg1.inputs_sha256(inp) == meta["inputs_sha256"]
+    k_pool = torch.from_numpy(inp["k_pool"]).to(gpu)
+    v_pool = torch.from_numpy(inp["v_pool"]).to(gpu)
+    slot_mapping = torch.from_numpy(gold["slot_mapping"]).to(gpu)
+    paged_ops.kv_append(k_pool, v_pool, torch.from_numpy(inp["k_new"]).to(gpu), torch.from_numpy(inp["v_new"]).to(gpu),
+                        slot_mapping)
+    nb = max(len(t) for t in inp["tables"])
+    tables = np.zeros((cfg1.BATCH, nb), dtype=np.int32)
+    for i, t in enumerate(inp["tables"]):
+        tables[i, :len(t)] = t
+    out = paged_ops.paged_decode(torch.from_numpy(inp["q"]).to(gpu), k_pool, v_pool, torch.from_numpy(tables).to(gpu),
+                                 torch.from_numpy(gold["context_lens"]).to(gpu))
+    torch.cuda.synchronize()
+    blocks = cfg1.touched_blocks(inp["tables"])
+    assert cfg1.blocks_sha256(k_pool.cpu().numpy(), v_pool.cpu().numpy(), blocks) == meta["pool_after_append_sha256"]
+    assert np.abs(values(out) - gold["out"]).max() < 2e-5
+
+
 @pytest.mark.parametrize("cfg", [2, 3])
 def test_decode_step_full_size(gpu, cfg):
     """Configs 2 (fp16 B=32) and 3 (bf16 B=256, churned pool): one layer's append + attention vs float64."""

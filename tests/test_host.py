@@ -1,0 +1,243 @@
+"""CPU tests of the host side: allocator, decode-context index math, copy-on-write
+bookkeeping, the C-ABI library's exports and host-side argument checks, and the rule
+that the product path never falls back to the CPU.
+
+No kernel runs here (no GPU): ABI calls below only take paths that return before any
+launch (empty work or rejected arguments).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import importlib.util
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from engine import _native, paged_ops
+from engine.kv_cache import PagedKVCache
+from oracle import paged_ref as ref
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mipaged.h"
+
+
+def tiny_paged(num_blocks=12, block_size=4, max_seqs=4, max_len=32, **kw) -> PagedKVCache:
+    return PagedKVCache(num_layers=1, num_kv_heads=2, head_dim=8, num_blocks=num_blocks, block_size=block_size,
+                        max_seqs=max_seqs, max_len=max_len, dtype=torch.float32, device="cpu", **kw)
+
+
+# ----------------------------------------------------------------------------- allocator (reference known answers)
+
+
+def test_paged_block_bookkeeping():
+    """tests/test_kv_cache.py:163-175 restated."""
+    cache = tiny_paged(num_blocks=6, block_size=4)
+    a = cache.allocate(5)
+    assert len(cache.block_tables[a]) == 2 and cache.num_free_blocks == 4
+    assert cache.ensure_capacity(a, 8) and len(cache.block_tables[a]) == 2
+    assert cache.ensure_capacity(a, 9) and len(cache.block_tables[a]) == 3
+    b = cache.allocate(12)
+    assert cache.num_free_blocks == 0
+    assert not cache.can_allocate(1) and not cache.ensure_capacity(b, 13)
+    cache.free(a)
+    assert cache.num_free_blocks == 3 and cache.can_allocate(12)
+    with pytest.raises(RuntimeError):
+        cache.free(a)
+
+
+def test_prefix_blocks_are_shared_refcounted_and_evicted_lru():
+    """tests/test_kv_cache.py:210-242 restated."""
+    cache = PagedKVCache(num_layers=1, num_kv_heads=1, head_dim=4, num_blocks=16, block_size=4, max_seqs=4,
+                         max_len=64, dtype=torch.float32, device="cpu", enable_prefix_caching=True)
+    shared = list(range(100, 116))
+    a_tokens = shared + [1, 2, 3]
+    a = cache.allocate(len(a_tokens), token_ids=a_tokens)
+    assert cache.lengths[a] == 0
+    cache.lengths[a] = len(a_tokens)
+    cache.register_prefix(a, a_tokens)
+    b_tokens = shared + [7, 8]
+    b = cache.allocate(len(b_tokens), token_ids=b_tokens)
+    assert cache.lengths[b] == 16
+    assert cache.block_tables[b][:4] == cache.block_tables[a][:4]
+    assert cache.block_tables[b][4] != cache.block_tables[a][4]
+    c = cache.allocate(16, token_ids=shared)
+    assert cache.lengths[c] == 12
+    cache.free(a)
+    cache.free(b)
+    cache.free(c)
+    assert cache.num_free_blocks == 16
+    d = cache.allocate(18, token_ids=shared + [5, 6])
+    assert cache.lengths[d] == 16
+    cache.free(d)
+    e = cache.allocate(64, token_ids=list(range(64)))
+    cache.free(e)
+    f = cache.allocate(18, token_ids=shared + [5, 6])
+    assert cache.lengths[f] == 0
+
+
+def test_slot_ids_and_lru_reuse_order():
+    """Slots from 0 upward; a freed uncached block is reused before older free blocks (kv_cache.py:468-488)."""
+    cache = tiny_paged(num_blocks=8, block_size=4)
+    s0, s1 = cache.allocate(8), cache.allocate(4)
+    assert (s0, s1) == (0, 1)
+    assert cache.block_tables[s0] == [0, 1] and cache.block_tables[s1] == [2]
+    cache.free(s0)  # releases 1 then 0, each to the head of the queue
+    s2 = cache.allocate(12)
+    assert cache.block_tables[s2] == [0, 1, 3]
+    assert s2 == 0  # the freed slot id is handed out again
+
+
+# ----------------------------------------------------------------------------- decode context index math
+
+
+def test_decode_context_matches_oracle_inputs():
+    cache = tiny_paged(num_blocks=12, block_size=4)
+    lengths = [6, 9, 3]
+    slots = [cache.allocate(0) for _ in lengths]
+    for n_blocks in range(1, 4):
+        for s, n in zip(slots, lengths):
+            cache.ensure_capacity(s, min(n + 1, n_blocks * 4))
+    for s, n in zip(slots, lengths):
+        cache.lengths[s] = n
+    ctx = cache.decode_context(slots)
+    tables = [cache.block_tables[s] for s in slots]
+    want = ref.decode_inputs(lengths, tables, 4)
+    assert ctx.positions.tolist() == want["positions"].tolist()
+    assert ctx.slot_mapping.tolist() == want["slot_mapping"].tolist()
+    assert ctx.write_blocks.tolist() == want["write_blocks"].tolist()
+    assert ctx.write_offsets.tolist() == want["write_offsets"].tolist()
+    assert ctx.context_lens.tolist() == want["context_lens"].tolist()
+    assert ctx.block_tables.tolist() == want["tables"].tolist()
+    assert ctx.block_tables.dtype == torch.int32 and ctx.context_lens.dtype == torch.int32
+    assert torch.equal(ctx.mask, torch.as_tensor(want["mask"])[:, None, None, :])
+    ctx.commit()
+    assert [cache.lengths[s] for s in slots] == [7, 10, 4]
+
+
+def test_decode_context_requires_capacity():
+    cache = tiny_paged(num_blocks=4, block_size=4)
+    s = cache.allocate(4)
+    cache.lengths[s] = 4  # next token needs a second block
+    with pytest.raises(ValueError):
+        cache.decode_context([s])
+
+
+def test_fork_copy_on_write_bookkeeping(monkeypatch):
+    """A write into a shared, partially filled block gets a private copy (one copy_blocks call)."""
+    cache = tiny_paged(num_blocks=10, block_size=4)
+    copies = []
+    monkeypatch.setattr(cache, "copy_blocks", lambda pairs: copies.append(list(pairs)))
+    parent = cache.allocate(7)
+    cache.lengths[parent] = 6  # blocks [0, 1]; block 1 holds tokens 4..5
+    child = cache.fork(parent)
+    assert cache.block_tables[child] == cache.block_tables[parent]
+    assert cache.ref_count(cache.block_tables[parent][1]) == 2
+    ctx = cache.decode_context([child])  # token 6 goes into shared block 1 -> copied
+    old = cache.block_tables[parent][1]
+    new = cache.block_tables[child][1]
+    assert copies == [[(old, new)]] and new != old
+    assert cache.ref_count(old) == 1 and cache.ref_count(new) == 1
+    assert cache.block_tables[child][0] == cache.block_tables[parent][0]  # full block stays shared
+    assert ctx.slot_mapping.tolist() == [new * 4 + 2]
+    cache.decode_context([parent])  # the parent's block is now private: no copy
+    assert len(copies) == 1
+
+
+def test_packed_prefill_slot_mapping():
+    cache = tiny_paged(num_blocks=12, block_size=4)
+    slots = [cache.allocate(0) for _ in range(2)]
+    ctx = cache.packed_prefill_context(slots, [5, 3])
+    blocks, offsets = ref.write_index(cache.block_tables, slots, [0, 0], [5, 3], 4)
+    assert ctx.slot_mapping.tolist() == (blocks * 4 + offsets).tolist()
+    assert ctx.positions.tolist() == [0, 1, 2, 3, 4, 0, 1, 2]
+
+
+# ----------------------------------------------------------------------------- C ABI
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"^\s*(?:const\s+char\s*\*|int|size_t)\s+(mip_\w+)\s*\(", text, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.LIB_PATH.exists():
+        spec = importlib.util.spec_from_file_location("mip_build", ROOT / "mini-inference_amd" / "build.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    return _native.load()
+
+
+def test_header_declares_the_bound_entry_points():
+    assert sorted(header_functions()) == sorted(_native.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(_native.LIB_PATH))
+    for name in header_functions():
+        assert hasattr(raw, name), f"{name} declared in mipaged.h but not exported"
+    assert lib.mip_version() >> 16 == 0 and lib.mip_version() & 0xFFFF >= 1
+    assert lib.mip_status_string(_native.MIP_OK) == b"ok"
+    assert lib.mip_status_string(_native.MIP_EINVAL) == b"invalid argument"
+    assert b"unsupported" in lib.mip_status_string(_native.MIP_EUNSUPPORTED)
+
+
+def test_abi_host_checks_return_before_launch(lib):
+    """Empty work returns OK and rejected arguments return EINVAL, with nothing launched."""
+    E, OK = _native.MIP_EINVAL, _native.MIP_OK
+    app = lib.mip_kv_append
+    args = [None, None, 128, 64, 128, 64, None, None, 16, None, 0, 2, 64, 16, _native.MIP_BF16, None]
+    assert app(*args) == OK                             # n_tokens = 0
+    assert app(*(args[:14] + [7, None])) == E           # unknown dtype
+    bad_bs = list(args); bad_bs[13] = 12
+    assert app(*bad_bs) == E                            # block size not a power of two
+    null = list(args); null[10] = 4
+    assert app(*null) == E                              # tokens but null pointers
+    dec = lib.mip_paged_decode
+    dargs = [None, 896, 64, None, 896, 64, None, None, 64, None, 8, None, 0, 14, 2, 64, 16, 8, 0.125, None, 0,
+             _native.MIP_BF16, None]
+    assert dec(*dargs) == OK                            # batch 0
+    g = list(dargs); g[12], g[14] = 4, 3
+    assert dec(*g) == E                                 # 14 heads do not split over 3 kv heads
+    st = list(dargs); st[12], st[10] = 4, 4
+    assert dec(*st) == E                                # table stride below max_blocks
+    nul = list(dargs); nul[12] = 4
+    assert dec(*nul) == E                               # null pointers
+    assert lib.mip_paged_decode_workspace(0, 14, 2, 64, 16, 8, _native.MIP_BF16) == 0
+    cp = lib.mip_copy_blocks
+    assert cp(None, None, None, 0, 24, 100, 8192, None) == OK
+    assert cp(None, None, None, 3, 0, 100, 8192, None) == E
+    assert cp(None, None, None, 3, 24, 100, 8192, None) == E
+
+
+# ----------------------------------------------------------------------------- no CPU fallback
+
+
+def test_kernels_refuse_cpu_tensors():
+    k = torch.zeros(5, 2, 4, 8)
+    v = torch.zeros_like(k)
+    with pytest.raises(RuntimeError):
+        paged_ops.kv_append(k, v, torch.zeros(1, 2, 8), torch.zeros(1, 2, 8), torch.zeros(1, dtype=torch.int64))
+    with pytest.raises(RuntimeError):
+        paged_ops.paged_decode(torch.zeros(1, 4, 8), k, v, torch.zeros(1, 1, dtype=torch.int32),
+                               torch.ones(1, dtype=torch.int32))
+    with pytest.raises(RuntimeError):
+        paged_ops.copy_blocks(k[None], v[None], torch.zeros(1, 2, dtype=torch.int64))
+
+
+def test_missing_library_raises(tmp_path):
+    with pytest.raises(_native.NativeLibraryMissing):
+        _native.load(tmp_path / "absent.so")
+
+
+def test_product_never_imports_the_oracle():
+    for src in (ROOT / "mini-inference_amd").rglob("*.py"):
+        text = src.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle", text, flags=re.M), src
+        assert "paged_ref" not in text, src
