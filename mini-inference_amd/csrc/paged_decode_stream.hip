@@ -45,13 +45,16 @@ namespace decode {
 namespace {
 
 #ifndef MIP_STREAM_WAVES
-#define MIP_STREAM_WAVES 2
+#define MIP_STREAM_WAVES 4
 #endif
 #ifndef MIP_STREAM_STAGES_D64
 #define MIP_STREAM_STAGES_D64 3
 #endif
 #ifndef MIP_STREAM_STAGES_D128
 #define MIP_STREAM_STAGES_D128 2
+#endif
+#ifndef MIP_STREAM_PRIO
+#define MIP_STREAM_PRIO 1
 #endif
 constexpr int kSW = MIP_STREAM_WAVES;   // wavefronts per workgroup
 constexpr int kStreamMaxBatch = 4096;   // context lengths + tile prefix fit in LDS
@@ -443,6 +446,22 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
       produce(ic<k>{}, scalar_table);
     });
     int i = lo;
+#if MIP_STREAM_PRIO
+    // Issue priority falls as the wavefront's own range progresses (3 in its first quarter
+    // ... 0 in its last). The arbiter otherwise favours older wavefronts, so the ones
+    // dispatched last on a CU fall behind and finish long after the rest.
+    const int span = hi - lo;
+    int quarter = 0;
+    __builtin_amdgcn_s_setprio(3);
+    auto reprioritise = [&]() __attribute__((always_inline)) {
+      const int q = ((i - lo) * 4) / span;
+      if (q == quarter) return;
+      quarter = q;
+      if (q == 1) __builtin_amdgcn_s_setprio(2);
+      else if (q == 2) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    };
+#endif
     // Step on stage k: load tile i+NS-1 into the stage freed last step, then compute tile i.
     auto step = [&](auto kc) __attribute__((always_inline)) -> bool {
       constexpr int k = decltype(kc)::value;
@@ -451,6 +470,9 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
       consume(ic<k>{}, i);
       if (++i >= hi) return false;
       advance(cb, ckvh, ct, cL, cn);
+#if MIP_STREAM_PRIO
+      reprioritise();
+#endif
       return true;
     };
     while (static_all<0, NS>(step)) {
