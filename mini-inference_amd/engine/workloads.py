@@ -12,6 +12,7 @@ pool-sized fills). The five shapes:
      by 5,000 alloc/free events before the 256 sequences are allocated
   4  fp16, 64 requests sharing a 520-token prefix (32 full blocks + a partial one, forked,
      so the partial block is copied on write), unique suffixes U[32, 512], packed append
+     (:func:`build_prefix_batch`)
   5  bf16, 28q/4kv heads, D 128, 28 layers, B 128, ctx log-uniform [512, 8192], block 32
 
 "ctx" is the number of tokens already cached; a decode step appends one, so a sequence
@@ -150,6 +151,45 @@ def build_decode_batch(shape: DecodeShape, device: torch.device | str, seed: int
             for layer in range(pool.shape[0]):
                 pool[layer].normal_(0.0, shape.kv_scale, generator=gen)
     return DecodeBatch(shape, cache, slots, ctx)
+
+
+@dataclass
+class PrefixBatch:
+    """A shared-prefix packed prefill: one parent holding the prefix, ``requests`` forks of it."""
+    cache: PagedKVCache
+    parent: int
+    children: list[int]
+    suffix_lens: list[int]
+    prefix_len: int
+
+
+def build_prefix_batch(device: torch.device | str, seed: int = 0, requests: int = 64, prefix_len: int = 520,
+                       suffix_lo: int = 32, suffix_hi: int = 512, num_layers: int = 24, num_kv_heads: int = 2,
+                       head_dim: int = 64, block_size: int = 16, dtype: torch.dtype = torch.float16,
+                       num_blocks: int | None = None) -> PrefixBatch:
+    """Shape 4: ``requests`` sequences forked from one parent whose ``prefix_len`` tokens are cached.
+
+    With the default 520 tokens the prefix fills 32 blocks of 16 and part of a 33rd, so every
+    fork shares 32 full blocks and one partially filled block; the first write of each fork's
+    suffix copies that partial block (copy-on-write). The pool holds N(0, 1) data and the
+    parent's prefix rows are part of it. Suffix lengths are U[suffix_lo, suffix_hi].
+    """
+    rng = random.Random(seed)
+    suffix_lens = [rng.randint(suffix_lo, suffix_hi) for _ in range(requests)]
+    bs = block_size
+    need = -(-prefix_len // bs) + sum(-(-(prefix_len + n) // bs) - prefix_len // bs for n in suffix_lens)
+    nb = num_blocks if num_blocks is not None else need + 64
+    max_len = prefix_len + suffix_hi
+    cache = PagedKVCache(num_layers, num_kv_heads, head_dim, nb, bs, max_seqs=requests + 1, max_len=max_len,
+                         dtype=dtype, device=device)
+    gen = torch.Generator(device=cache.k.device).manual_seed(seed + 2)
+    for pool in (cache.k, cache.v):
+        for layer in range(pool.shape[0]):
+            pool[layer].normal_(0.0, 1.0, generator=gen)
+    parent = cache.allocate(prefix_len)
+    cache.lengths[parent] = prefix_len
+    children = [cache.fork(parent) for _ in range(requests)]
+    return PrefixBatch(cache, parent, children, suffix_lens, prefix_len)
 
 
 def step_inputs(batch: DecodeBatch, seed: int = 0, device: torch.device | str | None = None):

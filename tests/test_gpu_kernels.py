@@ -302,9 +302,10 @@ def test_paged_decode_golden_fixture(gpu):
     assert np.abs(values(out) - gold["out"]).max() < 2e-5
 
 
-@pytest.mark.parametrize("cfg", [2, 3])
+@pytest.mark.parametrize("cfg", [2, 3, 5])
 def test_decode_step_full_size(gpu, cfg):
-    """Configs 2 (fp16 B=32) and 3 (bf16 B=256, churned pool): one layer's append + attention vs float64."""
+    """Configs 2 (fp16 B=32), 3 (bf16 B=256, churned pool) and 5 (bf16 28q/4kv D=128 BS=32 B=128):
+    one layer's append + attention vs float64."""
     from engine import workloads
 
     announce(f"config{cfg} decode step")
@@ -327,8 +328,45 @@ def test_decode_step_full_size(gpu, cfg):
     got = values(out[:, :, 0])
     err = np.abs(got - want).max()
     print(f"config{cfg} max-abs err {err:.3g}, max |out| {np.abs(want).max():.3g}")
-    assert err <= 2e-3  # plain max-abs: at these context lengths |out| < 0.5, so rounding fits too
+    assert err <= 2e-3  # plain max-abs: at these context lengths |out| < 1, where half a bf16 ulp is <= 1.95e-3
     assert attention_error(got, want, dname(shape.dtype)) <= 2e-3
+
+
+def test_prefix_fork_packed_append_copy_on_write(gpu):
+    """Config 4: 64 forks of a 520-token prefix, packed append of their suffixes (about 17k
+    tokens per layer) after copy-on-write of the shared partial block; every byte of both
+    pools (2 layers) vs the oracle replaying the same copies and appends."""
+    from engine import paged_ops, workloads
+
+    announce("config4 prefix fork + packed append + copy-on-write")
+    pb = workloads.build_prefix_batch(gpu, seed=0, num_layers=2)
+    cache = pb.cache
+    before_k, before_v = storage(cache.k), storage(cache.v)
+    parent_table = list(cache.block_tables[pb.parent])
+    assert len(parent_table) == 33 and all(cache.ref_count(b) == 65 for b in parent_table)
+    ctx = cache.packed_prefill_context(pb.children, pb.suffix_lens)  # ensure_capacity + copy-on-write
+    n_tok = sum(pb.suffix_lens)
+    gen = torch.Generator().manual_seed(7)
+    ks = [torch.randn(n_tok, 2, 64, generator=gen).to(torch.float16).to(gpu) for _ in range(2)]
+    vs = [torch.randn(n_tok, 2, 64, generator=gen).to(torch.float16).to(gpu) for _ in range(2)]
+    for layer in range(2):
+        paged_ops.kv_append(cache.k[layer], cache.v[layer], ks[layer], vs[layer], ctx.slot_mapping)
+    torch.cuda.synchronize()
+    # bookkeeping: 32 full prefix blocks still shared by all, the partial one now private per fork
+    for c in pb.children:
+        t = cache.block_tables[c]
+        assert t[:32] == parent_table[:32] and t[32] != parent_table[32]
+    assert all(cache.ref_count(b) == 65 for b in parent_table[:32]) and cache.ref_count(parent_table[32]) == 1
+    pairs = [(parent_table[32], cache.block_tables[c][32]) for c in pb.children]
+    assert len({d for _, d in pairs}) == len(pairs)
+    want_k, want_v = before_k.copy(), before_v.copy()
+    ref.copy_blocks(want_k, want_v, pairs)
+    blocks, offsets = ref.write_index(cache.block_tables, pb.children, [pb.prefix_len] * len(pb.children),
+                                      pb.suffix_lens, cache.block_size)
+    assert np.array_equal(blocks * cache.block_size + offsets, ctx.slot_mapping.cpu().numpy())
+    for layer in range(2):
+        ref.append(want_k[layer], want_v[layer], blocks, offsets, storage(ks[layer]), storage(vs[layer]))
+    assert np.array_equal(storage(cache.k), want_k) and np.array_equal(storage(cache.v), want_v)
 
 
 def test_decode_context_matches_per_sequence_sdpa(gpu):
