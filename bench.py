@@ -15,7 +15,9 @@ Reported (one JSON line on stdout):
                 around a timed loop of the calls), against the 8 TB/s HBM peak; traffic = measured
                 HBM bytes per call when a counter summary exists under profiles/
   decode_tok_s  B / full decode-step time of a random-init Qwen2.5-0.5B (embedding, 24 layers
-                with GEMMs, RoPE, append, attention, MLP, final norm, logits)
+                with GEMMs, RoPE, append, attention, MLP, final norm, logits), the step replayed
+                as one captured HIP graph (engine/cuda_graphs.py); decode_tok_s_eager: the same
+                step launched eagerly
   cpu_baseline  the reference's torch CPU path (index_put_ append + table gather + SDPA,
                 the oracle's restatement) timed on this host's cores for one layer, fp32
 
@@ -117,36 +119,60 @@ def cpu_baseline(batch, layer_q, layer_k, layer_v, budget_s: float) -> dict:
 
 
 def decode_tok_s(batch, steps: int, warmup: int) -> dict:
-    """Full random-init Qwen2.5-0.5B decode step at this batch, eager, through the cache contexts."""
+    """Full random-init Qwen2.5-0.5B decode step at this batch: eager, and replayed as one HIP graph.
+
+    A step = host tables + H2D, embedding, 24 layers (GEMMs, RoPE, KV append, paged
+    attention, MLP), final norm and logits, synchronised. Sequence lengths are restored after
+    every step, so each step appends at the same positions and attends the same contexts.
+    """
     import torch
 
+    from engine.cuda_graphs import GraphedDecoder
     from engine.model import Qwen2Config, Qwen2ForCausalLM, random_init_
 
     cfg = Qwen2Config.qwen2_5_0_5b()
-    dev = batch.cache.k.device
+    cache = batch.cache
+    dev = cache.k.device
     with torch.device(dev):
         model = Qwen2ForCausalLM(cfg)
     model = random_init_(model.to(dev, batch.shape.dtype), seed=0)
-    ids = torch.randint(0, cfg.vocab_size, (len(batch.slots), 1), device=dev,
-                        generator=torch.Generator(device=dev).manual_seed(5))
+    tokens = torch.randint(0, cfg.vocab_size, (len(batch.slots),), generator=torch.Generator().manual_seed(5))
+    ids = tokens.to(dev).unsqueeze(1)
+    lengths = {s: cache.lengths[s] for s in batch.slots}
 
     @torch.inference_mode()
-    def step():
-        ctx = batch.cache.decode_context(batch.slots)  # host tables + H2D, as the runner does each step
+    def eager_step():
+        ctx = cache.decode_context(batch.slots)  # host tables + H2D, as the runner does each step
         hidden = model(ids, ctx.positions.unsqueeze(1), ctx)
         return model.compute_logits(hidden[:, -1]).float()
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    times = []
-    for _ in range(steps):
-        t0 = time.perf_counter()
-        step()
+    graphed = GraphedDecoder(model, cache, max_batch=len(batch.slots))
+    graphed.capture(batches=[len(batch.slots)])
+    token_list = tokens.tolist()
+
+    @torch.inference_mode()
+    def graph_step():
+        out = graphed.decode(batch.slots, token_list)
+        cache.lengths.update(lengths)
+        return out
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
         torch.cuda.synchronize()
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    return {"tok_s": len(batch.slots) / t, "ms_per_step": t * 1e3, "steps": steps}
+        times = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times)
+
+    t_eager = timed(eager_step)
+    t_graph = timed(graph_step)
+    n = len(batch.slots)
+    return {"tok_s": n / t_graph, "ms_per_step": t_graph * 1e3, "eager_tok_s": n / t_eager,
+            "eager_ms_per_step": t_eager * 1e3, "steps": steps}
 
 
 def main() -> int:
@@ -276,7 +302,9 @@ def main() -> int:
             dm = decode_tok_s(batch, steps=max(10, min(args.steps, 30)), warmup=3)
             result["decode_tok_s"] = round(dm["tok_s"], 1)
             result["decode_ms_per_step"] = round(dm["ms_per_step"], 3)
-            log(f"full-model decode: {dm['ms_per_step']:.2f} ms/step, {dm['tok_s']:.0f} tok/s")
+            result["decode_tok_s_eager"] = round(dm["eager_tok_s"], 1)
+            log(f"full-model decode: graph {dm['ms_per_step']:.2f} ms/step ({dm['tok_s']:.0f} tok/s), "
+                f"eager {dm['eager_ms_per_step']:.2f} ms/step ({dm['eager_tok_s']:.0f} tok/s)")
         except Exception as exc:  # the headline kernel numbers stand on their own
             log(f"full-model decode failed: {exc!r}")
             result["decode_tok_s"] = None

@@ -1,0 +1,174 @@
+"""HIP-graph capture of the paged decode step (engine/cuda_graphs.py:1-189 of the reference).
+
+A decode step launches a few hundred small kernels (24 layers of norms, GEMMs, RoPE, the KV
+append and the paged attention); replaying them as one captured graph removes the host
+launch cost. As in the reference:
+
+* inputs live in static device buffers (token ids, positions, block tables) that are
+  overwritten before each replay;
+* one graph per batch bucket (1, 2, 4, 8, then every 16 up to ``max_batch``); rows past
+  the real batch point at the cache's scratch block, so their appends land there and their
+  outputs are ignored;
+* everything that depends on the inputs (slot mapping, context lengths) is computed inside
+  the graph from the static buffers.
+
+Unlike the reference, the attention kernel reads each sequence's pages in place and its
+launch shape does not depend on the KV length, so one KV bucket (the cache's ``max_len``)
+serves every step by default; ``kv_step`` restores per-length buckets (useful only for the
+partition kernels, whose grid grows with the longest table).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import numpy as np
+import torch
+
+from . import paged_ops
+from .kv_cache import PagedKVCache
+from .model import Qwen2ForCausalLM
+
+
+def _batch_buckets(limit: int) -> list[int]:
+    """1, 2, 4, 8, then every 16 up to ``limit`` (always including ``limit``); engine/cuda_graphs.py:34-43."""
+    sizes = [b for b in (1, 2, 4, 8) if b < limit] + list(range(16, limit, 16))
+    return sizes + [limit]
+
+
+def _kv_buckets(limit: int, step: int | None, block_size: int) -> list[int]:
+    """KV-length buckets in whole blocks: every ``step`` positions up to ``limit``, or just ``limit``."""
+    raw = [limit] if step is None else list(range(step, limit, step)) + [limit]
+    return sorted({-(-kv // block_size) * block_size for kv in raw})
+
+
+class _GraphDecodeContext:
+    """Attention for a captured decode step; reads everything from the static buffers."""
+
+    def __init__(self, owner: "GraphedDecoder", batch: int, kv_len: int) -> None:
+        self.cache = owner.cache
+        self.batch, self.kv_len = batch, kv_len
+        self.num_blocks = kv_len // owner.cache.block_size
+        self.positions = owner.positions[:batch]
+        self.tables = owner.tables[:batch, :self.num_blocks]
+        self.slot_mapping = owner.slot_mapping[:batch]
+        self.context_lens = owner.context_lens[:batch]
+        self.scale = 1.0 / (owner.cache.head_dim ** 0.5)
+
+    def prepare(self) -> None:
+        """Inside the graph, once per step: slot mapping and context lengths from the static buffers."""
+        bs = self.cache.block_size
+        write_blocks = self.tables.gather(1, torch.div(self.positions, bs, rounding_mode="floor").unsqueeze(1))
+        self.slot_mapping.copy_(write_blocks.squeeze(1).to(torch.int64) * bs + self.positions % bs)
+        self.context_lens.copy_(self.positions + 1)
+
+    def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
+        paged_ops.kv_append(k_layer, v_layer, k[:, :, 0], v[:, :, 0], self.slot_mapping)
+        out = paged_ops.paged_decode(q[:, :, 0], k_layer, v_layer, self.tables, self.context_lens, scale=self.scale,
+                                     max_blocks=self.num_blocks)
+        return out.unsqueeze(2)
+
+
+class GraphedDecoder:
+    """Captures the decode step as HIP graphs and replays them (engine/cuda_graphs.py:95-189).
+
+    Call :meth:`capture` once, then :meth:`decode` each step. ``decode`` returns ``None``
+    when no captured graph fits, and the caller runs the eager step instead.
+    """
+
+    def __init__(self, model: Qwen2ForCausalLM, cache: PagedKVCache, max_batch: int, kv_step: int | None = None) -> None:
+        if not isinstance(cache, PagedKVCache):
+            raise TypeError("GraphedDecoder drives the paged cache")
+        self.model, self.cache = model, cache
+        self.device = cache.k.device
+        self.batch_buckets = _batch_buckets(max_batch)
+        self.kv_buckets = _kv_buckets(cache.max_len, kv_step, cache.block_size)
+        top = self.batch_buckets[-1]
+        max_blocks = self.kv_buckets[-1] // cache.block_size
+        dev = self.device
+        self.ids = torch.zeros(top, 1, dtype=torch.long, device=dev)
+        self.positions = torch.zeros(top, dtype=torch.long, device=dev)
+        self.tables = torch.full((top, max_blocks), cache.scratch_block, dtype=torch.int32, device=dev)
+        self.slot_mapping = torch.zeros(top, dtype=torch.long, device=dev)
+        self.context_lens = torch.ones(top, dtype=torch.int32, device=dev)
+        # Host staging (pinned): ids and positions in one int64 row pair, tables as int32.
+        self._stage_i64 = torch.zeros(2, top, dtype=torch.long, pin_memory=True)
+        self._stage_tables = torch.full((top, max_blocks), cache.scratch_block, dtype=torch.int32, pin_memory=True)
+        # (batch, kv_len) -> (graph, its output logits, its context); the context stays alive
+        # with the graph because the graph reads its tensors.
+        self.graphs: dict[tuple[int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor, _GraphDecodeContext]] = {}
+        self._pool = None
+        self.replays = 0
+
+    @torch.inference_mode()
+    def capture(self, batches: Sequence[int] | None = None) -> None:
+        """Record one graph per (batch, kv length) bucket, largest first so smaller ones reuse its memory."""
+        wanted = self.batch_buckets if batches is None else sorted({self._bucket(b) for b in batches})
+        for batch in reversed(wanted):
+            for kv_len in reversed(self.kv_buckets):
+                self._capture_one(batch, kv_len)
+        torch.cuda.synchronize()
+
+    def _bucket(self, n: int) -> int:
+        b = next((b for b in self.batch_buckets if b >= n), None)
+        if b is None:
+            raise ValueError(f"batch {n} exceeds max_batch {self.batch_buckets[-1]}")
+        return b
+
+    def _capture_one(self, batch: int, kv_len: int) -> None:
+        ctx = _GraphDecodeContext(self, batch, kv_len)
+
+        def step() -> torch.Tensor:
+            ctx.prepare()
+            hidden = self.model(self.ids[:batch], self.positions[:batch].unsqueeze(1), ctx)
+            return self.model.compute_logits(hidden[:, -1]).float()
+
+        # Every row points at the scratch block while recording.
+        self.positions.zero_()
+        self.tables.fill_(self.cache.scratch_block)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up outside the graph: kernel selection, workspace, allocator
+            for _ in range(2):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool=self._pool):
+            logits = step()
+        self._pool = graph.pool()
+        self.graphs[(batch, kv_len)] = (graph, logits, ctx)
+
+    def decode(self, slots: Sequence[int], last_tokens: Sequence[int]) -> torch.Tensor | None:
+        """One decode step via a captured graph; logits ``[len(slots), vocab]``, or None if none fits."""
+        n = len(slots)
+        positions = [self.cache.lengths[s] for s in slots]
+        bs = self.cache.block_size
+        batch = next((b for b in self.batch_buckets if b >= n), None)
+        kv_len = next((k for k in self.kv_buckets if k > max(positions)), None)
+        if batch is None or kv_len is None or (batch, kv_len) not in self.graphs:
+            return None
+        if any(p // bs >= len(self.cache.block_tables[s]) for p, s in zip(positions, slots)):
+            raise ValueError("a sequence has no block for its next token (call ensure_capacity first)")
+        self.cache.prepare_writes(list(slots), positions, [1] * n)  # copy-on-write of shared blocks
+        graph, logits, _ = self.graphs[(batch, kv_len)]
+        nb = kv_len // bs
+        st, tb = self._stage_i64, self._stage_tables
+        st[0, :n] = torch.as_tensor(list(last_tokens), dtype=torch.long)
+        st[0, n:batch] = 0
+        st[1, :n] = torch.as_tensor(positions, dtype=torch.long)
+        st[1, n:batch] = 0
+        rows = np.full((batch, nb), self.cache.scratch_block, dtype=np.int32)
+        for i, s in enumerate(slots):
+            row = self.cache.block_tables[s][:nb]
+            rows[i, :len(row)] = row
+        tb[:batch, :nb].copy_(torch.from_numpy(rows))
+        self.ids[:batch, 0].copy_(st[0, :batch], non_blocking=True)
+        self.positions[:batch].copy_(st[1, :batch], non_blocking=True)
+        self.tables[:batch, :nb].copy_(tb[:batch, :nb], non_blocking=True)
+        graph.replay()
+        torch.cuda.current_stream().synchronize()  # the pinned staging rows are reused next step
+        self.replays += 1
+        for s in slots:
+            self.cache.lengths[s] += 1
+        return logits[:n]

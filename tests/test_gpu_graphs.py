@@ -1,0 +1,83 @@
+"""HIP-graph decode (engine/cuda_graphs.py) against the eager decode step, on the GPU.
+
+Two caches start from identical contents. Each step runs the eager path on one, replays the
+captured graph on the other, and compares the logits and the pools. Replays are separated by
+eager work and synchronisations, and every replay is checked.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(gpu, lengths, seed=0):
+    from engine.kv_cache import PagedKVCache
+    from engine.model import Qwen2Config, Qwen2ForCausalLM, random_init_
+
+    cfg = Qwen2Config(vocab_size=512, hidden_size=896, intermediate_size=1024, num_layers=2, num_heads=14,
+                      num_kv_heads=2, head_dim=64)
+    with torch.device(gpu):
+        model = Qwen2ForCausalLM(cfg)
+    model = random_init_(model.to(gpu, torch.bfloat16), seed=seed)
+    caches = []
+    for _ in range(2):
+        c = PagedKVCache(cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, num_blocks=256, block_size=16, max_seqs=16,
+                         max_len=512, dtype=torch.bfloat16, device=gpu)
+        slots = []
+        for n in lengths:
+            s = c.allocate(n + 8)  # room for the steps below
+            c.lengths[s] = n
+            slots.append(s)
+        caches.append((c, slots))
+    gen = torch.Generator(device=gpu).manual_seed(seed + 1)
+    for pool in (caches[0][0].k, caches[0][0].v):
+        pool.normal_(0.0, 1.0, generator=gen)
+    caches[1][0].k.copy_(caches[0][0].k)
+    caches[1][0].v.copy_(caches[0][0].v)
+    return model, caches
+
+
+@torch.inference_mode()
+def _run(gpu, lengths, batches, exact):
+    from engine.cuda_graphs import GraphedDecoder
+
+    model, ((ec, eslots), (gc, gslots)) = _setup(gpu, lengths)
+    assert eslots == gslots
+    gd = GraphedDecoder(model, gc, max_batch=16)
+    gd.capture(batches=batches)
+    tokens = [(7 * i + 3) % 512 for i in range(len(lengths))]
+    nb = ec.num_blocks  # the scratch block (index nb) takes the graph's padding rows
+    for step in range(4):
+        ctx = ec.decode_context(eslots)
+        ids = torch.tensor(tokens, device=gpu).unsqueeze(1)
+        want = model.compute_logits(model(ids, ctx.positions.unsqueeze(1), ctx)[:, -1]).float()
+        ctx.commit()
+        torch.cuda.synchronize()
+        got = gd.decode(gslots, tokens)
+        assert got is not None
+        torch.cuda.synchronize()
+        if exact:
+            assert torch.equal(got, want), f"step {step}: graph logits differ from eager"
+            assert torch.equal(gc.k[:, :nb], ec.k[:, :nb]) and torch.equal(gc.v[:, :nb], ec.v[:, :nb])
+        else:
+            # padded batch: the GEMMs see a different M, so allow their rounding differences
+            err = (got - want).abs().max().item()
+            assert err <= 1e-2 * want.abs().max().item() + 1e-3, f"step {step}: {err}"
+        assert [gc.lengths[s] for s in gslots] == [ec.lengths[s] for s in eslots]
+        tokens = want.argmax(dim=-1).tolist()
+    assert gd.replays == 4
+
+
+def test_graphed_decode_full_bucket_equals_eager(gpu):
+    announce("graphed decode, batch 8 = bucket 8, exact")
+    _run(gpu, [37, 100, 5, 64, 250, 17, 128, 300], batches=[8], exact=True)
+
+
+def test_graphed_decode_padded_bucket(gpu):
+    announce("graphed decode, batch 5 in bucket 8 (scratch-block padding rows)")
+    _run(gpu, [37, 100, 5, 64, 250], batches=[5], exact=False)

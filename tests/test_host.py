@@ -241,3 +241,18 @@ def test_product_never_imports_the_oracle():
         text = src.read_text()
         assert not re.search(r"^\s*(from|import)\s+oracle", text, flags=re.M), src
         assert "paged_ref" not in text, src
+
+
+# ----------------------------------------------------------------------------- graph buckets
+
+
+def test_graph_buckets():
+    """engine/cuda_graphs.py:34-47: batch buckets 1, 2, 4, 8, then every 16; KV buckets in whole blocks."""
+    from engine.cuda_graphs import _batch_buckets, _kv_buckets
+
+    assert _batch_buckets(256) == [1, 2, 4, 8] + list(range(16, 256, 16)) + [256]
+    assert _batch_buckets(5) == [1, 2, 4, 5]
+    assert _batch_buckets(8) == [1, 2, 4, 8]
+    assert _kv_buckets(1000, None, 16) == [1008]
+    assert _kv_buckets(1000, 256, 16) == [256, 512, 768, 1008]
+    assert _kv_buckets(520, 256, 32) == [256, 512, 544]
