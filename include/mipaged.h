@@ -111,7 +111,38 @@ int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h,
                      float scale, void* workspace, size_t workspace_bytes,
                      int32_t dtype, void* stream);
 
-/* Workspace bytes mip_paged_decode needs for this shape (0 when it needs none). */
+/*
+ * KV append + paged decode attention in one call: the whole of
+ *   PagedDecodeContext.attend   engine/kv_cache.py:611-620
+ * (scatter of the step's new K/V rows, then attention over every sequence's keys including
+ * the new one). The result, pool and output, is exactly that of mip_kv_append(k_new, v_new,
+ * ..., slot_mapping, n_tokens = batch, ...) followed by mip_paged_decode(...) with the same
+ * arguments.
+ *
+ * Where the stream kernel runs (16-bit K/V, head_dim 64/128, group <= 16) and the new rows
+ * and their strides are 16-byte aligned, no separate append kernel runs: the attention
+ * kernel reads each sequence's newest key straight from k_new / v_new, and its merge kernel
+ * (which follows it on the stream) copies the new rows into the pool. That needs
+ * slot_mapping[b] to be the slot of key context_lens[b] - 1 of sequence b (as
+ * PagedDecodeContext builds it) or outside the pool; a slot that some sequence reads as an
+ * older key is a race. Otherwise the append kernel and the decode run one after the other.
+ */
+int mip_paged_decode_append(const void* k_new, const void* v_new,
+                            int64_t k_stride_tok, int64_t k_stride_head,
+                            int64_t v_stride_tok, int64_t v_stride_head,
+                            const int64_t* slot_mapping,
+                            void* out, int64_t out_stride_b, int64_t out_stride_h,
+                            const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                            void* k_cache, void* v_cache, int64_t num_cache_blocks,
+                            const int32_t* block_tables, int64_t bt_stride,
+                            const int32_t* context_lens,
+                            int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
+                            float scale, void* workspace, size_t workspace_bytes,
+                            int32_t dtype, void* stream);
+
+/* Workspace bytes mip_paged_decode and mip_paged_decode_append need for this shape (0 when
+ * they need none). */
 size_t mip_paged_decode_workspace(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                   int32_t head_dim, int32_t block_size,
                                   int32_t max_blocks_per_seq, int32_t dtype);

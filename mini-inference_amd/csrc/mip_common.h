@@ -65,6 +65,10 @@ __device__ __forceinline__ int load_uniform_i32(const int32_t* p) {
   return *(const __attribute__((address_space(4))) int32_t*)(p);
 }
 
+__device__ __forceinline__ int64_t load_uniform_i64(const int64_t* p) {
+  return *(const __attribute__((address_space(4))) int64_t*)(p);
+}
+
 __host__ __device__ constexpr int ilog2_exact(int x) { return x <= 1 ? 0 : 1 + ilog2_exact(x >> 1); }
 
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }

@@ -824,12 +824,16 @@ extern "C" size_t mip_paged_decode_workspace(int32_t batch, int32_t num_heads, i
       ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype).bytes);
 }
 
-extern "C" int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h, const void* q,
-                                int64_t q_stride_b, int64_t q_stride_h, const void* k_cache, const void* v_cache,
-                                int64_t num_cache_blocks, const int32_t* block_tables, int64_t bt_stride,
-                                const int32_t* context_lens, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
-                                int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq, float scale,
-                                void* workspace, size_t workspace_bytes, int32_t dtype, void* stream) {
+namespace {
+
+// Decode attention; with app.slots set, the stream kernel also appends the step's new K/V
+// rows (the caller has checked their 16-byte alignment and that the stream kernel runs).
+int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, const void* q, int64_t q_stride_b,
+                      int64_t q_stride_h, const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
+                      const int32_t* block_tables, int64_t bt_stride, const int32_t* context_lens, int32_t batch,
+                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                      int32_t max_blocks_per_seq, float scale, void* workspace, size_t workspace_bytes,
+                      int32_t dtype, void* stream, const AppendRows& app) {
   if (dtype != MIP_F32 && dtype != MIP_F16 && dtype != MIP_BF16) return MIP_EINVAL;
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return MIP_EINVAL;
   if (num_heads % num_kv_heads != 0) return MIP_EINVAL;
@@ -895,10 +899,84 @@ extern "C" int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_str
     sa.group = group;
     sa.ws_prefix = reinterpret_cast<int*>(static_cast<char*>(workspace) + wl.prefix_off);
     sa.ws_rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.rec_off);
+    sa.app = app;
+    const int64_t lim = int64_t{1} << 31;
+    for (const int64_t x : {q_stride_b, q_stride_h, out_stride_b, out_stride_h, bt_stride, num_cache_blocks})
+      if (x <= -lim || x >= lim) return MIP_EUNSUPPORTED;
+    sa.q_sb = static_cast<int32_t>(q_stride_b);
+    sa.q_sh = static_cast<int32_t>(q_stride_h);
+    sa.out_sb = static_cast<int32_t>(out_stride_b);
+    sa.out_sh = static_cast<int32_t>(out_stride_h);
+    sa.bt_stride = static_cast<int32_t>(bt_stride);
+    sa.ncb = static_cast<int32_t>(num_cache_blocks);
     const int st = stream_launch(wl.stream, sa, dtype, head_dim, group, num_kv_heads, batch, s);
     return st == 0 ? MIP_OK : st;
   }
+  if (app.slots) return MIP_EUNSUPPORTED;  // callers fuse only into the stream kernel
   hipLaunchKernelGGL(kp.part, dim3(wl.nparts, num_kv_heads, batch), dim3(kNW * kWave), 0, s, a);
   if (wl.nparts > 1) hipLaunchKernelGGL(kp.merge, dim3(num_kv_heads, batch), dim3(256), 0, s, a);
   return status_from_hip(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h, const void* q,
+                                int64_t q_stride_b, int64_t q_stride_h, const void* k_cache, const void* v_cache,
+                                int64_t num_cache_blocks, const int32_t* block_tables, int64_t bt_stride,
+                                const int32_t* context_lens, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq, float scale,
+                                void* workspace, size_t workspace_bytes, int32_t dtype, void* stream) {
+  return paged_decode_impl(out, out_stride_b, out_stride_h, q, q_stride_b, q_stride_h, k_cache, v_cache,
+                           num_cache_blocks, block_tables, bt_stride, context_lens, batch, num_heads, num_kv_heads,
+                           head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, dtype, stream,
+                           AppendRows{});
+}
+
+extern "C" int mip_paged_decode_append(const void* k_new, const void* v_new, int64_t k_stride_tok,
+                                       int64_t k_stride_head, int64_t v_stride_tok, int64_t v_stride_head,
+                                       const int64_t* slot_mapping, void* out, int64_t out_stride_b,
+                                       int64_t out_stride_h, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                       void* k_cache, void* v_cache, int64_t num_cache_blocks,
+                                       const int32_t* block_tables, int64_t bt_stride, const int32_t* context_lens,
+                                       int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                       int32_t block_size, int32_t max_blocks_per_seq, float scale, void* workspace,
+                                       size_t workspace_bytes, int32_t dtype, void* stream) {
+  if (dtype != MIP_F32 && dtype != MIP_F16 && dtype != MIP_BF16) return MIP_EINVAL;
+  if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return MIP_EINVAL;
+  if (batch == 0) return MIP_OK;
+  if (!k_new || !v_new || !slot_mapping) return MIP_EINVAL;
+  const int64_t es = dtype == MIP_F32 ? 4 : 2;
+  const uint64_t align = reinterpret_cast<uintptr_t>(k_new) | reinterpret_cast<uintptr_t>(v_new) |
+                         static_cast<uint64_t>(k_stride_tok * es) | static_cast<uint64_t>(k_stride_head * es) |
+                         static_cast<uint64_t>(v_stride_tok * es) | static_cast<uint64_t>(v_stride_head * es) |
+                         static_cast<uint64_t>(head_dim * es);
+  const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
+  const int64_t lim = int64_t{1} << 31;
+  bool strides_fit = true;
+  for (const int64_t x : {k_stride_tok * es, k_stride_head * es, v_stride_tok * es, v_stride_head * es})
+    strides_fit = strides_fit && x > -lim && x < lim;
+  if (wl.algo == Algo::kStream && (align & 15) == 0 && strides_fit && batch <= 65535) {
+    AppendRows app{};
+    app.k = static_cast<const char*>(k_new);
+    app.v = static_cast<const char*>(v_new);
+    app.k_st = static_cast<int32_t>(k_stride_tok * es);
+    app.k_sh = static_cast<int32_t>(k_stride_head * es);
+    app.v_st = static_cast<int32_t>(v_stride_tok * es);
+    app.v_sh = static_cast<int32_t>(v_stride_head * es);
+    app.slots = slot_mapping;
+    app.k_cache = static_cast<char*>(k_cache);
+    app.v_cache = static_cast<char*>(v_cache);
+    return paged_decode_impl(out, out_stride_b, out_stride_h, q, q_stride_b, q_stride_h, k_cache, v_cache,
+                             num_cache_blocks, block_tables, bt_stride, context_lens, batch, num_heads,
+                             num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, workspace,
+                             workspace_bytes, dtype, stream, app);
+  }
+  // Not fusable here: the append kernel, then the decode, in stream order.
+  const int st = mip_kv_append(k_new, v_new, k_stride_tok, k_stride_head, v_stride_tok, v_stride_head, k_cache,
+                               v_cache, num_cache_blocks, slot_mapping, batch, num_kv_heads, head_dim, block_size,
+                               dtype, stream);
+  if (st != MIP_OK) return st;
+  return mip_paged_decode(out, out_stride_b, out_stride_h, q, q_stride_b, q_stride_h, k_cache, v_cache,
+                          num_cache_blocks, block_tables, bt_stride, context_lens, batch, num_heads, num_kv_heads,
+                          head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, dtype, stream);
 }

@@ -30,6 +30,17 @@ struct DecodeArgs {
   float* ws_ml;   // [B][Hq][nparts][2]
 };
 
+// The step's new K/V rows, appended by the stream kernel itself (mip_paged_decode_append).
+// slots == nullptr: no append.
+struct AppendRows {
+  const char* k;               // row (b, h) at k + b * k_st + h * k_sh (bytes), head_dim elements
+  const char* v;
+  int32_t k_st, k_sh, v_st, v_sh;
+  const int64_t* slots;        // [batch] flat pool slot of sequence b's new token
+  char* k_cache;               // the pool (same as DecodeArgs k / v, writable)
+  char* v_cache;
+};
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -85,6 +96,10 @@ struct StreamArgs {
   int group;
   int tw;          // wavefronts in the grid
   int min_tiles;   // fewest tiles an active wavefront takes
+  AppendRows app;
+  // 32-bit copies of the 64-bit strides / sizes of DecodeArgs (the host checks they fit), so
+  // the stream kernel's loop state stays within the scalar register file.
+  int32_t q_sb, q_sh, out_sb, out_sh, bt_stride, ncb;
   int rec_stride;  // floats per record: m[16] | l[16] | acc[group][D]
   int* ws_prefix;  // [batch + 1] tile prefix over sequences (written by workgroup 0)
   float* ws_rec;   // [tw][2][rec_stride]

@@ -149,7 +149,7 @@ __device__ __forceinline__ bool static_all(F&& f) {
   return true;
 }
 
-template <int DT, int D, int QR, int NS>
+template <int DT, int D, int QR, int NS, bool FUSED>
 __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa) {
   using R = Ring<D, QR>;
   using Ops = MfmaOps<DT>;
@@ -167,6 +167,8 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int i16 = lane & 15, grp = lane >> 4;
   const int cap = a.max_blocks * a.bs;
+
+  const AppendRows& ap = sa.app;
 
   // ---- work split: context lengths -> tile prefix (block-wide exclusive scan).
   for (int i = tid; i < B; i += kSW * kWave) {
@@ -227,6 +229,9 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
   int cL = seq_len(cb);
   int cn = (cL + 15) >> 4;
   int pb = cb, pkvh = ckvh, pt = ct, pL = cL, pn = cn;  // producer cursor (next tile to load)
+  // Fused append: the new token's slot of the producer's sequence, fetched when the producer
+  // enters the sequence so it has arrived by the sequence's last tile.
+  int64_t p_slot = FUSED ? load_uniform_i64(ap.slots + pb) : -1;
   auto advance = [&](int& b_, int& kvh_, int& t_, int& L_, int& n_) __attribute__((always_inline)) {
     if (++t_ < n_) return;
     t_ = 0;
@@ -260,46 +265,60 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     constexpr int s = decltype(stage_c)::value;
     lchar_t* st = ring_ptr + s * R::STAGE;
     const int tb = 16 * pt;
-    const int32_t* table = a.bt + static_cast<int64_t>(pb) * a.bt_stride;
+    const int32_t* table = a.bt + static_cast<int64_t>(pb) * sa.bt_stride;
     if constexpr (decltype(scalar_table)::value) {
       // block_size >= 16: the tile lies in one block.
       const int blk = load_uniform_i32(table + (tb >> a.log2_bs));
-      const bool bok = blk >= 0 && blk < a.ncb;
+      const bool bok = blk >= 0 && blk < sa.ncb;
       const int rem = pL - tb;
       const int nvalid = bok ? (rem < 16 ? rem : 16) : 0;
       vmask[s] = nvalid >= 16 ? 0xffffu : ((1u << nvalid) - 1u);
       const int64_t row0 = static_cast<int64_t>((bok ? blk : 0) * a.hkv + pkvh) * a.bs + (tb & (a.bs - 1));
+      // The segment's last tile holds the newest key (position pL - 1); with a fused append
+      // whose slot is that key's slot, its row comes from the new-row source.
+      int nr = -1;
+      if (FUSED && pt == pn - 1 && bok) {
+        const int64_t want = static_cast<int64_t>(blk) * a.bs + ((pL - 1) & (a.bs - 1));
+        if (p_slot == want) nr = pL - 1 - tb;
+      }
+      const char* nk = ap.k + static_cast<int64_t>(pb) * ap.k_st + static_cast<int64_t>(pkvh) * ap.k_sh;
+      const char* nv = ap.v + static_cast<int64_t>(pb) * ap.v_st + static_cast<int64_t>(pkvh) * ap.v_sh;
 #pragma unroll
       for (int j = 0; j < R::KI; ++j) {
         const int r = j * RPD + dma_r;
         const int64_t row = row0 + (r < nvalid ? r : 0);
         const int lc = dma_pc ^ (r & (CPR - 1));
-        dma16(a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
-        dma16(a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
+        const bool fresh = r == nr;
+        dma16(fresh ? nk + lc * 16 : a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
+        dma16(fresh ? nv + dma_pc * 16 : a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
       }
     } else {
       // Small blocks: every row looks its block up; rows that are not keys re-read the
       // tile's first key (block 0 if even that id is out of range, which the mask drops).
       const int tk0 = tb;
       const int b0 = table[tk0 >> a.log2_bs];
-      const bool ok0 = b0 >= 0 && b0 < a.ncb;
+      const bool ok0 = b0 >= 0 && b0 < sa.ncb;
       const int64_t row_first = static_cast<int64_t>((ok0 ? b0 : 0) * a.hkv + pkvh) * a.bs + (tk0 & (a.bs - 1));
       {
         const int tok = tb + i16;
         const int bl = table[(tok < pL ? tok : tk0) >> a.log2_bs];
-        const bool ok = tok < pL && bl >= 0 && bl < a.ncb;
+        const bool ok = tok < pL && bl >= 0 && bl < sa.ncb;
         vmask[s] = static_cast<uint32_t>(__ballot(ok)) & 0xffffu;
       }
+      const int64_t new_slot = (FUSED && pt == pn - 1) ? p_slot : -1;
+      const char* nk = ap.k + static_cast<int64_t>(pb) * ap.k_st + static_cast<int64_t>(pkvh) * ap.k_sh;
+      const char* nv = ap.v + static_cast<int64_t>(pb) * ap.v_st + static_cast<int64_t>(pkvh) * ap.v_sh;
 #pragma unroll
       for (int j = 0; j < R::KI; ++j) {
         const int r = j * RPD + dma_r;
         const int tok = tb + r;
         const int bl = table[(tok < pL ? tok : tk0) >> a.log2_bs];
-        const bool ok = tok < pL && bl >= 0 && bl < a.ncb;
+        const bool ok = tok < pL && bl >= 0 && bl < sa.ncb;
         const int64_t row = ok ? static_cast<int64_t>(bl * a.hkv + pkvh) * a.bs + (tok & (a.bs - 1)) : row_first;
         const int lc = dma_pc ^ (r & (CPR - 1));
-        dma16(a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
-        dma16(a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
+        const bool fresh = ok && tok == pL - 1 && static_cast<int64_t>(bl) * a.bs + (tok & (a.bs - 1)) == new_slot;
+        dma16(fresh ? nk + lc * 16 : a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
+        dma16(fresh ? nv + dma_pc * 16 : a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
       }
     }
 #pragma unroll
@@ -307,7 +326,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
       const int hr = j * RPD + dma_r;
       const int hh = hr < G ? hr : 0;
       const int lc = dma_pc ^ (hr & (CPR - 1));
-      dma16(a.q + (static_cast<int64_t>(pb) * a.q_sb + static_cast<int64_t>(pkvh * G + hh) * a.q_sh) * 2 + lc * 16,
+      dma16(a.q + (static_cast<int64_t>(pb) * sa.q_sb + static_cast<int64_t>(pkvh * G + hh) * sa.q_sh) * 2 + lc * 16,
             st + R::Q_OFF + j * 1024);
     }
   };
@@ -409,7 +428,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
       if (full_start && ct == cn - 1) {
         if (live) {
           const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-          S* orow = out_base + static_cast<int64_t>(cb) * a.out_sb + static_cast<int64_t>(ckvh * G + i16) * a.out_sh;
+          S* orow = out_base + static_cast<int64_t>(cb) * sa.out_sb + static_cast<int64_t>(ckvh * G + i16) * sa.out_sh;
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             const uint32_t w0 = Ops::pack2(acc[mt][0] * inv, acc[mt][1] * inv);
@@ -436,7 +455,11 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
   // The producer cursor moves to tile x only while x < hi; past the end it stays on the
   // last tile, which is loaded again so every stage issues the same number of loads.
   auto adv_p = [&](int x) __attribute__((always_inline)) {
-    if (x < hi) advance(pb, pkvh, pt, pL, pn);
+    if (x < hi) {
+      const int ob = pb;
+      advance(pb, pkvh, pt, pL, pn);
+      if (FUSED && pb != ob && pb < B) p_slot = load_uniform_i64(ap.slots + pb);
+    }
   };
   auto run = [&](auto scalar_table) __attribute__((always_inline)) {
     // Prologue: tiles lo .. lo+NS-2 into stages 0 .. NS-2.
@@ -487,7 +510,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
 }
 
 // Combine the pieces of every segment the stream kernel split. Grid (kv heads, batch).
-template <int DT, int D>
+template <int DT, int D, bool FUSED>
 __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) {
   using S = typename Elem<DT>::S;
   const int64_t REC = sa.rec_stride;
@@ -495,6 +518,22 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
   const int kvh = blockIdx.x, b = blockIdx.y, G = sa.group;
   S* out_base = reinterpret_cast<S*>(a.out);
   const int cap = a.max_blocks * a.bs;
+  // Fused append: copy sequence b's new K and V rows of this kv head into the pool. The
+  // stream kernel, which ran before this one, took the newest key straight from the source,
+  // so nothing reads these pool rows in this call.
+  const AppendRows& ap = sa.app;
+  if (FUSED && threadIdx.x < 2 * (D * 2 / 16)) {
+    constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
+    const int side = threadIdx.x / CPR, c = threadIdx.x % CPR;
+    const int64_t slot = ap.slots[b];
+    if (slot >= 0 && slot < a.ncb * a.bs) {
+      const char* src = side ? ap.v + static_cast<int64_t>(b) * ap.v_st + static_cast<int64_t>(kvh) * ap.v_sh
+                             : ap.k + static_cast<int64_t>(b) * ap.k_st + static_cast<int64_t>(kvh) * ap.k_sh;
+      char* dst = (side ? ap.v_cache : ap.k_cache) +
+                  (((slot >> a.log2_bs) * a.hkv + kvh) * a.bs + (slot & (a.bs - 1))) * (D * 2);
+      *reinterpret_cast<uint4*>(dst + c * 16) = *reinterpret_cast<const uint4*>(src + c * 16);
+    }
+  }
   int L = a.lens[b];
   L = L < cap ? L : cap;
   if (L <= 0) {
@@ -607,13 +646,21 @@ using StreamFn = void (*)(StreamArgs);
 struct StreamPick {
   StreamFn main = nullptr;
   StreamFn merge = nullptr;
+  StreamFn main_fused = nullptr;   // with the step's K/V append (mip_paged_decode_append)
+  StreamFn merge_fused = nullptr;
   int ring_bytes = 0;  // per wavefront
 };
 
 template <int DT, int D, int QR>
 StreamPick pick_one() {
   constexpr int NS = D == 64 ? MIP_STREAM_STAGES_D64 : MIP_STREAM_STAGES_D128;
-  return {paged_decode_stream<DT, D, QR, NS>, paged_decode_stream_merge<DT, D>, NS * Ring<D, QR>::STAGE};
+  StreamPick p;
+  p.main = paged_decode_stream<DT, D, QR, NS, false>;
+  p.merge = paged_decode_stream_merge<DT, D, false>;
+  p.main_fused = paged_decode_stream<DT, D, QR, NS, true>;
+  p.merge_fused = paged_decode_stream_merge<DT, D, true>;
+  p.ring_bytes = NS * Ring<D, QR>::STAGE;
+  return p;
 }
 
 StreamPick pick(int dtype, int d, int group) {
@@ -666,8 +713,9 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, i
   sa.tw = cfg.tw;
   sa.min_tiles = stream_min_tiles();
   sa.rec_stride = static_cast<int>(cfg.rec_floats);
-  hipLaunchKernelGGL(p.main, dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
-  hipLaunchKernelGGL(p.merge, dim3(num_kv_heads, batch), dim3(256), 0, stream, sa);
+  const bool fused = sa.app.slots != nullptr;
+  hipLaunchKernelGGL(fused ? p.main_fused : p.main, dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
+  hipLaunchKernelGGL(fused ? p.merge_fused : p.merge, dim3(num_kv_heads, batch), dim3(256), 0, stream, sa);
   return static_cast<int>(hipGetLastError());
 }
 

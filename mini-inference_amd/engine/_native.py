@@ -20,6 +20,7 @@ EXPORTED = (
     "mip_status_string",
     "mip_kv_append",
     "mip_paged_decode",
+    "mip_paged_decode_append",
     "mip_paged_decode_workspace",
     "mip_copy_blocks",
 )
@@ -37,6 +38,12 @@ _SIGNATURES = {
     "mip_paged_decode": (
         _c.c_int,
         [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
+         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _i32, _vp],
+    ),
+    "mip_paged_decode_append": (
+        _c.c_int,
+        [_vp, _vp, _i64, _i64, _i64, _i64, _vp,
+         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
          _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _i32, _vp],
     ),
     "mip_paged_decode_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),

@@ -64,9 +64,9 @@ class _GraphDecodeContext:
 
     def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
-        paged_ops.kv_append(k_layer, v_layer, k[:, :, 0], v[:, :, 0], self.slot_mapping)
-        out = paged_ops.paged_decode(q[:, :, 0], k_layer, v_layer, self.tables, self.context_lens, scale=self.scale,
-                                     max_blocks=self.num_blocks)
+        out = paged_ops.paged_decode_append(q[:, :, 0], k[:, :, 0], v[:, :, 0], k_layer, v_layer, self.slot_mapping,
+                                            self.tables, self.context_lens, scale=self.scale,
+                                            max_blocks=self.num_blocks)
         return out.unsqueeze(2)
 
 

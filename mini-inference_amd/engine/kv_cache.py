@@ -6,8 +6,8 @@ Drop-in for the paged half of the reference's engine/kv_cache.py:
   API (engine/kv_cache.py:377-579) with the same block-reuse policy, so the scheduler,
   prefix caching and graph code see the same block ids. It adds :meth:`copy_blocks`
   and :meth:`fork` for copy-on-write of shared blocks.
-* :class:`PagedDecodeContext` (engine/kv_cache.py:582-624): ``attend`` = KV append
-  kernel + paged decode-attention kernel. No gathered copy of the history is made.
+* :class:`PagedDecodeContext` (engine/kv_cache.py:582-624): ``attend`` = KV append +
+  paged decode attention in one fused call. No gathered copy of the history is made.
 * :class:`PackedPrefillContext` (engine/kv_cache.py:218-301): the packed scatter is the
   append kernel; the prefill attention itself stays in torch SDPA.
 
@@ -318,10 +318,11 @@ class PagedDecodeContext:
         return self._mask
 
     def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """Append this step's k/v and attend (engine/kv_cache.py:611-620) in one fused call."""
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
-        paged_ops.kv_append(k_layer, v_layer, k[:, :, 0], v[:, :, 0], self.slot_mapping)
-        out = paged_ops.paged_decode(q[:, :, 0], k_layer, v_layer, self.block_tables, self.context_lens,
-                                     scale=self.scale, max_blocks=self.num_blocks)
+        out = paged_ops.paged_decode_append(q[:, :, 0], k[:, :, 0], v[:, :, 0], k_layer, v_layer, self.slot_mapping,
+                                            self.block_tables, self.context_lens, scale=self.scale,
+                                            max_blocks=self.num_blocks)
         return out.unsqueeze(2)
 
     def commit(self) -> None:

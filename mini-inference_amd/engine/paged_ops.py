@@ -133,8 +133,13 @@ def decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_d
 
 def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                          context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
-                         max_blocks: int | None = None, workspace: torch.Tensor | None = None):
-    """Validate a :func:`paged_decode` call once; returns ``(PreparedCall, out)``."""
+                         max_blocks: int | None = None, workspace: torch.Tensor | None = None,
+                         append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None):
+    """Validate a :func:`paged_decode` call once; returns ``(PreparedCall, out)``.
+
+    ``append = (k, v, slot_mapping)`` prepares the fused append + decode call
+    (:func:`paged_decode_append`) instead.
+    """
     _require_device(q, k_cache, v_cache, block_tables, context_lens)
     if q.dim() != 3 or q.stride(2) != 1:
         raise ValueError("q must be [B, Hq, D] with a contiguous last dimension")
@@ -175,7 +180,21 @@ def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
             k_cache.data_ptr(), v_cache.data_ptr(), nb, block_tables.data_ptr(), block_tables.stride(0),
             context_lens.data_ptr(), b, hq, hkv, d, bs, mb, scale, ws_ptr, ws_bytes, code, _stream_ptr(q.device))
     keep = (out, q, k_cache, v_cache, block_tables, context_lens, workspace)
-    return PreparedCall(lib.mip_paged_decode, args, "mip_paged_decode", keep), out
+    if append is None:
+        return PreparedCall(lib.mip_paged_decode, args, "mip_paged_decode", keep), out
+    k, v, slot_mapping = append
+    _require_device(k, v, slot_mapping)
+    if k.shape != (b, hkv, d) or v.shape != (b, hkv, d):
+        raise ValueError(f"k/v must be [{b}, {hkv}, {d}], got {tuple(k.shape)} and {tuple(v.shape)}")
+    if k.dtype != k_cache.dtype or v.dtype != k_cache.dtype:
+        raise TypeError("k, v and the cache must share one dtype")
+    if k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("the last (head_dim) dimension of k/v must be contiguous")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.shape != (b,) or not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be contiguous int64 [B]")
+    fused = (k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1), slot_mapping.data_ptr(),
+             *args)
+    return PreparedCall(lib.mip_paged_decode_append, fused, "mip_paged_decode_append", keep + (k, v, slot_mapping)), out
 
 
 def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
@@ -191,6 +210,21 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     """
     call, out = prepare_paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, out, max_blocks,
                                      workspace)
+    call()
+    return out
+
+
+def paged_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                        v_cache: torch.Tensor, slot_mapping: torch.Tensor, block_tables: torch.Tensor,
+                        context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
+                        max_blocks: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`kv_append` of the step's ``k``/``v`` ``[B, Hkv, D]`` at ``slot_mapping``, then
+    :func:`paged_decode`, as one call (engine/kv_cache.py:611-620). One kernel launch on the
+    stream-kernel path; ``slot_mapping[b]`` must be the slot of key ``context_lens[b] - 1``
+    (or outside the pool).
+    """
+    call, out = prepare_paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, out, max_blocks,
+                                     workspace, append=(k, v, slot_mapping))
     call()
     return out
 

@@ -235,6 +235,56 @@ def test_paged_decode_never_reads_stale_rows(gpu, dtype, algo):
     _check_decode(gpu, dtype, len(lens), 14, 2, 64, 16, lens, seed=11, stale=float("nan"))
 
 
+@pytest.mark.parametrize("dtype,d,hq,hkv,bs", [("bfloat16", 64, 14, 2, 16), ("float16", 128, 28, 4, 32),
+                                               ("bfloat16", 64, 14, 2, 4), ("float32", 64, 14, 2, 16),
+                                               ("bfloat16", 128, 16, 1, 8), ("float16", 64, 8, 8, 64)])
+def test_fused_append_decode_equals_two_calls(gpu, dtype, d, hq, hkv, bs, algo):
+    """mip_paged_decode_append == mip_kv_append then mip_paged_decode: pools and outputs bit-identical.
+
+    Rows cover: the newest key in the first / middle / last row of its tile, a one-key
+    sequence, an empty sequence, a padding row (slot -1) and a row whose slot is a free block
+    (not the newest key's slot), which the fused kernel must write without redirecting.
+    """
+    from engine import paged_ops
+
+    announce(f"fused append+decode {dtype} d={d} hq={hq} hkv={hkv} bs={bs} algo={algo}")
+    if hq // hkv > 8 and (dtype == "float32" or algo == "valu"):
+        pytest.skip("query groups above 8 exist only in the MFMA kernels")
+    lens = [1, bs, bs + 1, 37, 513, 1200, 2049, 5, 0, 64, 17]  # keys after the append (positions + 1)
+    batch = len(lens)
+    q, k_pool, v_pool, tables, bt, width = _random_case(dtype, batch, hq, hkv, d, bs, lens, nb_extra=4, seed=d + bs)
+    nb = k_pool.shape[0] - 1
+    used = {blk for t in tables for blk in t}
+    free = [blk for blk in range(nb) if blk not in used]
+    slots = []
+    for b, n in enumerate(lens):
+        if n == 0 or b == 7:
+            slots.append(-1)                                  # no append for this row
+        elif b == 9:
+            slots.append(free[0] * bs + 3)                    # valid slot, but not the newest key's
+        else:
+            slots.append(tables[b][(n - 1) // bs] * bs + (n - 1) % bs)
+    g = torch.Generator().manual_seed(99)
+    dt = DTYPES[dtype]
+    wide = torch.randn(batch, 3 * hkv * d, generator=g).to(dt).to(gpu)
+    k_new = wide[:, hkv * d:2 * hkv * d].view(batch, hkv, d)  # strided view, as from a fused projection
+    v_new = torch.randn(batch, hkv, d, generator=g).to(dt).to(gpu)
+    slot_t = torch.tensor(slots, dtype=torch.int64, device=gpu)
+    bt_t = torch.from_numpy(bt).to(gpu)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=gpu)
+    qg = q.to(gpu)
+    ka, va = k_pool.to(gpu), v_pool.to(gpu)
+    kb, vb = ka.clone(), va.clone()
+    paged_ops.kv_append(ka, va, k_new, v_new, slot_t)
+    out_a = paged_ops.paged_decode(qg, ka, va, bt_t, lens_t, max_blocks=width)
+    out_b = paged_ops.paged_decode_append(qg, k_new, v_new, kb, vb, slot_t, bt_t, lens_t, max_blocks=width)
+    torch.cuda.synchronize()
+    assert torch.equal(ka, kb) and torch.equal(va, vb), "pools differ"
+    assert torch.equal(out_a, out_b), "outputs differ"
+    want = ref.attention_f64(values(q), values(ka), values(va), tables, lens, bs)
+    assert attention_error(values(out_b), want, dtype) <= TOL[dtype]
+
+
 def test_paged_decode_large_logits_rescale(gpu):
     """Scores spanning hundreds of units exercise the lazy running-max rescale."""
     from engine import paged_ops

@@ -210,6 +210,13 @@ def test_abi_host_checks_return_before_launch(lib):
     nul = list(dargs); nul[12] = 4
     assert dec(*nul) == E                               # null pointers
     assert lib.mip_paged_decode_workspace(0, 14, 2, 64, 16, 8, _native.MIP_BF16) == 0
+    fused = lib.mip_paged_decode_append
+    app = [None, None, 128, 64, 128, 64, None]
+    assert fused(*(app + dargs)) == OK                  # batch 0
+    nul = list(dargs); nul[12] = 4
+    assert fused(*(app + nul)) == E                     # new rows missing
+    bad = list(dargs); bad[21] = 9
+    assert fused(*(app + bad)) == E                     # unknown dtype
     cp = lib.mip_copy_blocks
     assert cp(None, None, None, 0, 24, 100, 8192, None) == OK
     assert cp(None, None, None, 3, 0, 100, 8192, None) == E
