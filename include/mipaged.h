@@ -100,6 +100,11 @@ int mip_kv_append(const void* k_src, const void* v_src,
  * current, and be 256-byte aligned. It needs no initialisation and its contents are
  * undefined afterwards; calls on one stream may reuse it, calls that can run
  * concurrently must not share it.
+ *
+ * `plan` (may be NULL) is a work plan made by mip_paged_decode_plan from the same
+ * context_lens and block_tables contents and the same shape, earlier on the stream; the
+ * kernel then starts from it instead of deriving its work split itself (every layer of a
+ * decode step shares one plan). It is ignored where the stream kernel does not run.
  */
 int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h,
                      const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -109,7 +114,7 @@ int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h,
                      int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                      int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
                      float scale, void* workspace, size_t workspace_bytes,
-                     int32_t dtype, void* stream);
+                     const void* plan, int32_t dtype, void* stream);
 
 /*
  * KV append + paged decode attention in one call: the whole of
@@ -139,7 +144,30 @@ int mip_paged_decode_append(const void* k_new, const void* v_new,
                             int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                             int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
                             float scale, void* workspace, size_t workspace_bytes,
-                            int32_t dtype, void* stream);
+                            const void* plan, int32_t dtype, void* stream);
+
+/*
+ * Work plan of the decode kernels for one decode step (no reference counterpart: the
+ * reference derives nothing per step beyond PagedDecodeContext's tensors,
+ * engine/kv_cache.py:592-609).
+ *
+ * Every layer of a step attends the same sequences, so the stream kernel's work split
+ * (each wavefront's range of key tiles and start position, the first tiles' block ids,
+ * and which pieces the merge combines) is the same for all of them. One launch of a single
+ * workgroup writes it; pass the plan to each layer's mip_paged_decode /
+ * mip_paged_decode_append, which then skip that work. Returns MIP_EUNSUPPORTED (nothing
+ * launched) for shapes the stream kernel does not run; mip_paged_decode_plan_bytes returns
+ * 0 for those. The plan is int32 data, 4-byte aligned, and stays valid while
+ * context_lens, block_tables and the shape do not change.
+ */
+size_t mip_paged_decode_plan_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int32_t block_size,
+                                   int32_t max_blocks_per_seq, int32_t dtype);
+int mip_paged_decode_plan(const int32_t* context_lens, const int32_t* block_tables,
+                          int64_t bt_stride, int32_t batch, int32_t num_heads,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int32_t max_blocks_per_seq, int32_t dtype, void* plan,
+                          size_t plan_bytes, void* stream);
 
 /* Workspace bytes mip_paged_decode and mip_paged_decode_append need for this shape (0 when
  * they need none). */

@@ -833,7 +833,7 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
                       const int32_t* block_tables, int64_t bt_stride, const int32_t* context_lens, int32_t batch,
                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                       int32_t max_blocks_per_seq, float scale, void* workspace, size_t workspace_bytes,
-                      int32_t dtype, void* stream, const AppendRows& app) {
+                      const void* plan, int32_t dtype, void* stream, const AppendRows& app) {
   if (dtype != MIP_F32 && dtype != MIP_F16 && dtype != MIP_BF16) return MIP_EINVAL;
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return MIP_EINVAL;
   if (num_heads % num_kv_heads != 0) return MIP_EINVAL;
@@ -900,6 +900,8 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
     sa.ws_prefix = reinterpret_cast<int*>(static_cast<char*>(workspace) + wl.prefix_off);
     sa.ws_rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.rec_off);
     sa.app = app;
+    sa.plan = static_cast<const int32_t*>(plan);
+    if (reinterpret_cast<uintptr_t>(plan) & 3) return MIP_EINVAL;
     const int64_t lim = int64_t{1} << 31;
     for (const int64_t x : {q_stride_b, q_stride_h, out_stride_b, out_stride_h, bt_stride, num_cache_blocks})
       if (x <= -lim || x >= lim) return MIP_EUNSUPPORTED;
@@ -925,11 +927,12 @@ extern "C" int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_str
                                 int64_t num_cache_blocks, const int32_t* block_tables, int64_t bt_stride,
                                 const int32_t* context_lens, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                 int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq, float scale,
-                                void* workspace, size_t workspace_bytes, int32_t dtype, void* stream) {
+                                void* workspace, size_t workspace_bytes, const void* plan, int32_t dtype,
+                                void* stream) {
   return paged_decode_impl(out, out_stride_b, out_stride_h, q, q_stride_b, q_stride_h, k_cache, v_cache,
                            num_cache_blocks, block_tables, bt_stride, context_lens, batch, num_heads, num_kv_heads,
-                           head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, dtype, stream,
-                           AppendRows{});
+                           head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, plan, dtype,
+                           stream, AppendRows{});
 }
 
 extern "C" int mip_paged_decode_append(const void* k_new, const void* v_new, int64_t k_stride_tok,
@@ -940,7 +943,7 @@ extern "C" int mip_paged_decode_append(const void* k_new, const void* v_new, int
                                        const int32_t* block_tables, int64_t bt_stride, const int32_t* context_lens,
                                        int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                        int32_t block_size, int32_t max_blocks_per_seq, float scale, void* workspace,
-                                       size_t workspace_bytes, int32_t dtype, void* stream) {
+                                       size_t workspace_bytes, const void* plan, int32_t dtype, void* stream) {
   if (dtype != MIP_F32 && dtype != MIP_F16 && dtype != MIP_BF16) return MIP_EINVAL;
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return MIP_EINVAL;
   if (batch == 0) return MIP_OK;
@@ -969,7 +972,7 @@ extern "C" int mip_paged_decode_append(const void* k_new, const void* v_new, int
     return paged_decode_impl(out, out_stride_b, out_stride_h, q, q_stride_b, q_stride_h, k_cache, v_cache,
                              num_cache_blocks, block_tables, bt_stride, context_lens, batch, num_heads,
                              num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, workspace,
-                             workspace_bytes, dtype, stream, app);
+                             workspace_bytes, plan, dtype, stream, app);
   }
   // Not fusable here: the append kernel, then the decode, in stream order.
   const int st = mip_kv_append(k_new, v_new, k_stride_tok, k_stride_head, v_stride_tok, v_stride_head, k_cache,
@@ -978,5 +981,36 @@ extern "C" int mip_paged_decode_append(const void* k_new, const void* v_new, int
   if (st != MIP_OK) return st;
   return mip_paged_decode(out, out_stride_b, out_stride_h, q, q_stride_b, q_stride_h, k_cache, v_cache,
                           num_cache_blocks, block_tables, bt_stride, context_lens, batch, num_heads, num_kv_heads,
-                          head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, dtype, stream);
+                          head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, plan, dtype,
+                          stream);
+}
+
+extern "C" size_t mip_paged_decode_plan_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                              int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
+                                              int32_t dtype) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+      max_blocks_per_seq <= 0 || num_heads % num_kv_heads != 0)
+    return 0;
+  const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
+  if (wl.algo != Algo::kStream) return 0;
+  return static_cast<size_t>(stream_plan_bytes(wl.stream, batch, num_kv_heads));
+}
+
+extern "C" int mip_paged_decode_plan(const int32_t* context_lens, const int32_t* block_tables, int64_t bt_stride,
+                                     int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t block_size, int32_t max_blocks_per_seq, int32_t dtype, void* plan,
+                                     size_t plan_bytes, void* stream) {
+  if (dtype != MIP_F32 && dtype != MIP_F16 && dtype != MIP_BF16) return MIP_EINVAL;
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return MIP_EINVAL;
+  if (num_heads % num_kv_heads != 0) return MIP_EINVAL;
+  if (!is_pow2(block_size) || block_size > 4096 || max_blocks_per_seq <= 0 || bt_stride < max_blocks_per_seq)
+    return MIP_EINVAL;
+  if (static_cast<int64_t>(max_blocks_per_seq) * block_size >= (int64_t{1} << 30)) return MIP_EINVAL;
+  if (!context_lens || !block_tables || !plan || (reinterpret_cast<uintptr_t>(plan) & 3)) return MIP_EINVAL;
+  const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
+  if (wl.algo != Algo::kStream) return MIP_EUNSUPPORTED;
+  if (plan_bytes < static_cast<size_t>(stream_plan_bytes(wl.stream, batch, num_kv_heads))) return MIP_EINVAL;
+  const int st = stream_plan_launch(wl.stream, context_lens, block_tables, bt_stride, batch, num_kv_heads, block_size,
+                                    max_blocks_per_seq, static_cast<int32_t*>(plan), static_cast<hipStream_t>(stream));
+  return st == 0 ? MIP_OK : st;
 }

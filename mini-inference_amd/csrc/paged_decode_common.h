@@ -97,6 +97,7 @@ struct StreamArgs {
   int tw;          // wavefronts in the grid
   int min_tiles;   // fewest tiles an active wavefront takes
   AppendRows app;
+  const int32_t* plan;  // stream work plan for these context lengths (nullptr: derive it in-kernel)
   // 32-bit copies of the 64-bit strides / sizes of DecodeArgs (the host checks they fit), so
   // the stream kernel's loop state stays within the scalar register file.
   int32_t q_sb, q_sh, out_sb, out_sh, bt_stride, ncb;
@@ -111,6 +112,19 @@ struct SShape {
   static constexpr int MT = D / 16;
   static constexpr int TILE_BYTES = 16 * D * 2;
 };
+
+// Layout of a stream work plan (int32 words), written once per step by the plan kernel:
+//   [0] T total tiles, [1] W active wavefronts, [2] batch, [3] kv heads, [4..7] unused;
+//   then W wavefront records of kPlanWave words: lo, hi (global tiles), b, kvh, t (start
+//   cursor), L (clamped length of b), nh (block-id hints), h0, h1 (block ids of the first
+//   tiles, block size >= 16 only);
+//   then batch * kv heads segment records of kPlanSeg words: g_lo (first wavefront holding a
+//   piece), R (pieces), lo_split (the first piece sits in that wavefront's "last segment"
+//   slot), L.
+constexpr int kPlanHeader = 8;
+constexpr int kPlanWave = 16;
+constexpr int kPlanSeg = 4;
+constexpr int kPlanHints = 2;
 
 __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
 #pragma unroll
@@ -139,6 +153,10 @@ struct StreamConfig {
 StreamConfig stream_config(int dtype, int d, int group, int batch);
 int stream_launch(const StreamConfig& cfg, const StreamArgs& sa, int dtype, int d, int group, int num_kv_heads,
                   int batch, hipStream_t stream);
+// Bytes of a work plan for this launch shape, and the plan kernel (one workgroup).
+int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads);
+int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32_t* block_tables, int64_t bt_stride,
+                       int batch, int num_kv_heads, int block_size, int max_blocks, int32_t* plan, hipStream_t stream);
 
 }  // namespace decode
 }  // namespace mip

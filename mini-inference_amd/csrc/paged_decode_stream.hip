@@ -149,7 +149,7 @@ __device__ __forceinline__ bool static_all(F&& f) {
   return true;
 }
 
-template <int DT, int D, int QR, int NS, bool FUSED>
+template <int DT, int D, int QR, int NS, bool FUSED, bool PLANNED>
 __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa) {
   using R = Ring<D, QR>;
   using Ops = MfmaOps<DT>;
@@ -170,63 +170,79 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
 
   const AppendRows& ap = sa.app;
 
-  // ---- work split: context lengths -> tile prefix (block-wide exclusive scan).
-  for (int i = tid; i < B; i += kSW * kWave) {
-    int L = a.lens[i];
-    L = L < cap ? L : cap;
-    s_len[i] = L > 0 ? L : 0;
-  }
-  __syncthreads();
-  {
-    const int chunk = (B + kSW * kWave - 1) / (kSW * kWave);
-    const int beg = tid * chunk < B ? tid * chunk : B;
-    const int end = beg + chunk < B ? beg + chunk : B;
-    int sum = 0;
-    for (int i = beg; i < end; ++i) sum += (s_len[i] + 15) >> 4;
-    const int incl = wave_inclusive_scan(sum, lane);
-    if (lane == kWave - 1) s_wtot[w] = incl;
-    __syncthreads();
-    int off = 0;
-    for (int j = 0; j < w; ++j) off += s_wtot[j];
-    int run = off + incl - sum;
-    for (int i = beg; i < end; ++i) {
-      s_pre[i] = run;
-      run += (s_len[i] + 15) >> 4;
-    }
-    if (tid == kSW * kWave - 1) s_pre[B] = off + incl;
-  }
-  __syncthreads();
-  const int total = a.hkv * s_pre[B];
-  if (blockIdx.x == 0) {
-    for (int i = tid; i <= B; i += kSW * kWave) sa.ws_prefix[i] = s_pre[i];
-  }
-  const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
-  const int gw = blockIdx.x * kSW + w;
-  const bool active = total > 0 && gw < tw;
-  int lo = 0, hi = 0, cb = 0, ckvh = 0, ct = 0;
-  if (active) {
-    lo = static_cast<int>(static_cast<int64_t>(gw) * total / tw);
-    hi = static_cast<int>(static_cast<int64_t>(gw + 1) * total / tw);
-    int lb = 0, ub = B - 1;  // largest b with Hkv * P[b] <= lo; its segment is not empty
-    while (lb < ub) {
-      const int mid = (lb + ub + 1) >> 1;
-      if (a.hkv * __builtin_amdgcn_readfirstlane(s_pre[mid]) <= lo) lb = mid; else ub = mid - 1;
-    }
-    cb = lb;
-    const int n = __builtin_amdgcn_readfirstlane((s_len[cb] + 15) >> 4);
-    const int rem = lo - a.hkv * __builtin_amdgcn_readfirstlane(s_pre[cb]);
-    ckvh = rem / n;
-    ct = rem - ckvh * n;
-  }
-  __syncthreads();  // the rings below reuse the scan area
-  if (!active || lo >= hi) return;
-
   auto seq_len = [&](int b) __attribute__((always_inline)) {
     int L = load_uniform_i32(a.lens + b);
     L = L < cap ? L : cap;
     return L > 0 ? L : 0;
   };
-  int cL = seq_len(cb);
+  const int gw = blockIdx.x * kSW + w;
+  int lo = 0, hi = 0, cb = 0, ckvh = 0, ct = 0, cL = 0;
+  int hint_n = 0, hint0 = 0, hint1 = 0;  // block ids of the first tiles (from a plan)
+  if constexpr (PLANNED) {
+    // ---- work split from the step's plan: this wavefront's range and start cursor.
+    if (gw >= load_uniform_i32(sa.plan + 1)) return;
+    const int32_t* pr = sa.plan + kPlanHeader + static_cast<int64_t>(gw) * kPlanWave;
+    lo = load_uniform_i32(pr + 0);
+    hi = load_uniform_i32(pr + 1);
+    cb = load_uniform_i32(pr + 2);
+    ckvh = load_uniform_i32(pr + 3);
+    ct = load_uniform_i32(pr + 4);
+    cL = load_uniform_i32(pr + 5);
+    hint_n = load_uniform_i32(pr + 6);
+    hint0 = load_uniform_i32(pr + 7);
+    hint1 = load_uniform_i32(pr + 8);
+    if (lo >= hi) return;
+  } else {
+    // ---- work split: context lengths -> tile prefix (block-wide exclusive scan).
+    for (int i = tid; i < B; i += kSW * kWave) {
+      int L = a.lens[i];
+      L = L < cap ? L : cap;
+      s_len[i] = L > 0 ? L : 0;
+    }
+    __syncthreads();
+    {
+      const int chunk = (B + kSW * kWave - 1) / (kSW * kWave);
+      const int beg = tid * chunk < B ? tid * chunk : B;
+      const int end = beg + chunk < B ? beg + chunk : B;
+      int sum = 0;
+      for (int i = beg; i < end; ++i) sum += (s_len[i] + 15) >> 4;
+      const int incl = wave_inclusive_scan(sum, lane);
+      if (lane == kWave - 1) s_wtot[w] = incl;
+      __syncthreads();
+      int off = 0;
+      for (int j = 0; j < w; ++j) off += s_wtot[j];
+      int run = off + incl - sum;
+      for (int i = beg; i < end; ++i) {
+        s_pre[i] = run;
+        run += (s_len[i] + 15) >> 4;
+      }
+      if (tid == kSW * kWave - 1) s_pre[B] = off + incl;
+    }
+    __syncthreads();
+    const int total = a.hkv * s_pre[B];
+    if (blockIdx.x == 0) {
+      for (int i = tid; i <= B; i += kSW * kWave) sa.ws_prefix[i] = s_pre[i];
+    }
+    const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
+    const bool active = total > 0 && gw < tw;
+    if (active) {
+      lo = static_cast<int>(static_cast<int64_t>(gw) * total / tw);
+      hi = static_cast<int>(static_cast<int64_t>(gw + 1) * total / tw);
+      int lb = 0, ub = B - 1;  // largest b with Hkv * P[b] <= lo; its segment is not empty
+      while (lb < ub) {
+        const int mid = (lb + ub + 1) >> 1;
+        if (a.hkv * __builtin_amdgcn_readfirstlane(s_pre[mid]) <= lo) lb = mid; else ub = mid - 1;
+      }
+      cb = lb;
+      const int n = __builtin_amdgcn_readfirstlane((s_len[cb] + 15) >> 4);
+      const int rem = lo - a.hkv * __builtin_amdgcn_readfirstlane(s_pre[cb]);
+      ckvh = rem / n;
+      ct = rem - ckvh * n;
+    }
+    __syncthreads();  // the rings below reuse the scan area
+    if (!active || lo >= hi) return;
+    cL = seq_len(cb);
+  }
   int cn = (cL + 15) >> 4;
   int pb = cb, pkvh = ckvh, pt = ct, pL = cL, pn = cn;  // producer cursor (next tile to load)
   // Fused append: the new token's slot of the producer's sequence, fetched when the producer
@@ -261,14 +277,16 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
 
   uint32_t vmask[NS];  // per stage: bit r = key row r of the tile is a key of its segment
 
-  auto produce = [&](auto stage_c, auto scalar_table) __attribute__((always_inline)) {
+  // hint: the tile's block id when the plan already looked it up (prologue only).
+  auto produce = [&](auto stage_c, auto scalar_table, bool has_hint = false, int hint = 0)
+                     __attribute__((always_inline)) {
     constexpr int s = decltype(stage_c)::value;
     lchar_t* st = ring_ptr + s * R::STAGE;
     const int tb = 16 * pt;
     const int32_t* table = a.bt + static_cast<int64_t>(pb) * sa.bt_stride;
     if constexpr (decltype(scalar_table)::value) {
       // block_size >= 16: the tile lies in one block.
-      const int blk = load_uniform_i32(table + (tb >> a.log2_bs));
+      const int blk = has_hint ? hint : load_uniform_i32(table + (tb >> a.log2_bs));
       const bool bok = blk >= 0 && blk < sa.ncb;
       const int rem = pL - tb;
       const int nvalid = bok ? (rem < 16 ? rem : 16) : 0;
@@ -466,7 +484,11 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     static_for<0, NS - 1>([&](auto kc) __attribute__((always_inline)) {
       constexpr int k = decltype(kc)::value;
       if constexpr (k > 0) adv_p(lo + k);
-      produce(ic<k>{}, scalar_table);
+      if constexpr (PLANNED && k < kPlanHints) {
+        produce(ic<k>{}, scalar_table, k < hint_n, k == 0 ? hint0 : hint1);
+      } else {
+        produce(ic<k>{}, scalar_table);
+      }
     });
     int i = lo;
 #if MIP_STREAM_PRIO
@@ -510,7 +532,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
 }
 
 // Combine the pieces of every segment the stream kernel split. Grid (kv heads, batch).
-template <int DT, int D, bool FUSED>
+template <int DT, int D, bool FUSED, bool PLANNED>
 __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) {
   using S = typename Elem<DT>::S;
   const int64_t REC = sa.rec_stride;
@@ -534,23 +556,37 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
       *reinterpret_cast<uint4*>(dst + c * 16) = *reinterpret_cast<const uint4*>(src + c * 16);
     }
   }
-  int L = a.lens[b];
-  L = L < cap ? L : cap;
+  int L, gw_lo, gw_hi;
+  bool lo_split;
+  if constexpr (PLANNED) {
+    const int W = load_uniform_i32(sa.plan + 1);
+    const int32_t* sd = sa.plan + kPlanHeader + static_cast<int64_t>(W) * kPlanWave +
+                        (static_cast<int64_t>(b) * a.hkv + kvh) * kPlanSeg;
+    gw_lo = load_uniform_i32(sd + 0);
+    gw_hi = gw_lo + load_uniform_i32(sd + 1) - 1;
+    lo_split = load_uniform_i32(sd + 2) != 0;
+    L = load_uniform_i32(sd + 3);
+  } else {
+    L = a.lens[b];
+    L = L < cap ? L : cap;
+  }
   if (L <= 0) {
     for (int i = threadIdx.x; i < G * D; i += blockDim.x)
       out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + i / D) * a.out_sh + i % D] =
           from_f32<DT>(0.0f);
     return;
   }
-  const int total = a.hkv * sa.ws_prefix[sa.batch];
-  const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
-  const int n = (L + 15) >> 4;
-  const int64_t s0 = static_cast<int64_t>(a.hkv) * sa.ws_prefix[b] + static_cast<int64_t>(kvh) * n;
-  const int64_t e1 = s0 + n - 1;
-  const int gw_lo = static_cast<int>(((s0 + 1) * tw - 1) / total);
-  const int gw_hi = static_cast<int>(((e1 + 1) * tw - 1) / total);
-  if (gw_lo == gw_hi) return;  // one wavefront held the whole segment and wrote it
-  const bool lo_split = static_cast<int64_t>(gw_lo) * total / tw < s0;
+  if constexpr (!PLANNED) {
+    const int total = a.hkv * sa.ws_prefix[sa.batch];
+    const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
+    const int n = (L + 15) >> 4;
+    const int64_t s0 = static_cast<int64_t>(a.hkv) * sa.ws_prefix[b] + static_cast<int64_t>(kvh) * n;
+    const int64_t e1 = s0 + n - 1;
+    gw_lo = static_cast<int>(((s0 + 1) * tw - 1) / total);
+    gw_hi = static_cast<int>(((e1 + 1) * tw - 1) / total);
+    lo_split = static_cast<int64_t>(gw_lo) * total / tw < s0;
+  }
+  if (gw_lo >= gw_hi) return;  // one wavefront held the whole segment and wrote it
   const int R = gw_hi - gw_lo + 1;
   // Record r of this segment: the first piece sits in the "last segment" slot of wavefront
   // gw_lo when that wavefront started inside an earlier segment, every other piece in the
@@ -641,13 +677,130 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
   }
 }
 
+// ---- the per-step work plan (mip_paged_decode_plan): one workgroup computes, from the
+// context lengths and block tables, the split the stream kernel would otherwise derive in
+// every call: wavefront ranges and start cursors, the first tiles' block ids, and every
+// segment's merge descriptor. Layout: kPlanHeader / kPlanWave / kPlanSeg.
+constexpr int kPlanThreads = 1024;
+
+struct PlanArgs {
+  const int32_t* lens;
+  const int32_t* bt;
+  int64_t bt_stride;
+  int32_t* plan;
+  int batch, hkv, bs, log2_bs, cap, tw, min_tiles;
+};
+
+__global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArgs p) {
+  extern __shared__ __attribute__((aligned(16))) char psm[];
+  const int B = p.batch;
+  int* s_len = reinterpret_cast<int*>(psm);  // [B] clamped context lengths
+  int* s_pre = s_len + B;                     // [B + 1] exclusive tile prefix
+  int* s_wtot = s_pre + B + 1;                // [kPlanThreads / kWave]
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  for (int i = tid; i < B; i += kPlanThreads) {
+    int L = p.lens[i];
+    L = L < p.cap ? L : p.cap;
+    s_len[i] = L > 0 ? L : 0;
+  }
+  __syncthreads();
+  {
+    const int chunk = (B + kPlanThreads - 1) / kPlanThreads;
+    const int beg = tid * chunk < B ? tid * chunk : B;
+    const int end = beg + chunk < B ? beg + chunk : B;
+    int sum = 0;
+    for (int i = beg; i < end; ++i) sum += (s_len[i] + 15) >> 4;
+    const int incl = wave_inclusive_scan(sum, lane);
+    if (lane == kWave - 1) s_wtot[w] = incl;
+    __syncthreads();
+    int off = 0;
+    for (int j = 0; j < w; ++j) off += s_wtot[j];
+    int run = off + incl - sum;
+    for (int i = beg; i < end; ++i) {
+      s_pre[i] = run;
+      run += (s_len[i] + 15) >> 4;
+    }
+    if (tid == kPlanThreads - 1) s_pre[B] = off + incl;
+  }
+  __syncthreads();
+  const int64_t T = static_cast<int64_t>(p.hkv) * s_pre[B];
+  const int W = T > 0 ? stream_active_waves(p.tw, static_cast<int>(T), p.min_tiles) : 0;
+  if (tid == 0) {
+    p.plan[0] = static_cast<int32_t>(T);
+    p.plan[1] = W;
+    p.plan[2] = B;
+    p.plan[3] = p.hkv;
+  }
+  // Wavefront records: the same split and cursor arithmetic as the in-kernel path.
+  for (int g = tid; g < W; g += kPlanThreads) {
+    const int lo = static_cast<int>(static_cast<int64_t>(g) * T / W);
+    const int hi = static_cast<int>(static_cast<int64_t>(g + 1) * T / W);
+    int lb = 0, ub = B - 1;  // largest b with Hkv * P[b] <= lo
+    while (lb < ub) {
+      const int mid = (lb + ub + 1) >> 1;
+      if (p.hkv * s_pre[mid] <= lo) lb = mid; else ub = mid - 1;
+    }
+    int b = lb, L = s_len[b], n = (L + 15) >> 4;
+    const int rem = lo - p.hkv * s_pre[b];
+    int kvh = rem / n, t = rem - kvh * n;
+    int32_t* r = p.plan + kPlanHeader + static_cast<int64_t>(g) * kPlanWave;
+    r[0] = lo;
+    r[1] = hi;
+    r[2] = b;
+    r[3] = kvh;
+    r[4] = t;
+    r[5] = L;
+    // Block ids of the first tiles the producer stages (block size >= 16 only: then a tile
+    // lies in one block). The cursor moves exactly as the stream kernel's producer does.
+    int nh = 0;
+    if (p.bs >= 16) {
+      for (int k = 0; k < kPlanHints; ++k) {
+        if (k > 0 && lo + k < hi) {
+          if (++t >= n) {
+            t = 0;
+            if (++kvh >= p.hkv) {
+              kvh = 0;
+              do {
+                ++b;
+                L = b < B ? s_len[b] : 16;
+                n = (L + 15) >> 4;
+              } while (n == 0);
+            }
+          }
+        }
+        r[7 + k] = p.bt[static_cast<int64_t>(b) * p.bt_stride + ((16 * t) >> p.log2_bs)];
+        ++nh;
+      }
+    }
+    r[6] = nh;
+  }
+  // Segment records for the merge kernel.
+  int32_t* seg = p.plan + kPlanHeader + static_cast<int64_t>(W) * kPlanWave;
+  for (int sidx = tid; sidx < B * p.hkv; sidx += kPlanThreads) {
+    const int b = sidx / p.hkv, kvh = sidx - b * p.hkv;
+    const int L = s_len[b], n = (L + 15) >> 4;
+    int g_lo = 0, R = 0, lo_split = 0;
+    if (n > 0) {
+      const int64_t s0 = static_cast<int64_t>(p.hkv) * s_pre[b] + static_cast<int64_t>(kvh) * n;
+      const int64_t e1 = s0 + n - 1;
+      g_lo = static_cast<int>(((s0 + 1) * W - 1) / T);
+      const int g_hi = static_cast<int>(((e1 + 1) * W - 1) / T);
+      R = g_hi - g_lo + 1;
+      lo_split = static_cast<int64_t>(g_lo) * T / W < s0 ? 1 : 0;
+    }
+    int32_t* r = seg + static_cast<int64_t>(sidx) * kPlanSeg;
+    r[0] = g_lo;
+    r[1] = R;
+    r[2] = lo_split;
+    r[3] = L;
+  }
+}
+
 using StreamFn = void (*)(StreamArgs);
 
 struct StreamPick {
-  StreamFn main = nullptr;
-  StreamFn merge = nullptr;
-  StreamFn main_fused = nullptr;   // with the step's K/V append (mip_paged_decode_append)
-  StreamFn merge_fused = nullptr;
+  StreamFn main[2][2] = {};   // [fused: with the step's K/V append][planned: from a work plan]
+  StreamFn merge[2][2] = {};
   int ring_bytes = 0;  // per wavefront
 };
 
@@ -655,10 +808,14 @@ template <int DT, int D, int QR>
 StreamPick pick_one() {
   constexpr int NS = D == 64 ? MIP_STREAM_STAGES_D64 : MIP_STREAM_STAGES_D128;
   StreamPick p;
-  p.main = paged_decode_stream<DT, D, QR, NS, false>;
-  p.merge = paged_decode_stream_merge<DT, D, false>;
-  p.main_fused = paged_decode_stream<DT, D, QR, NS, true>;
-  p.merge_fused = paged_decode_stream_merge<DT, D, true>;
+  p.main[0][0] = paged_decode_stream<DT, D, QR, NS, false, false>;
+  p.main[0][1] = paged_decode_stream<DT, D, QR, NS, false, true>;
+  p.main[1][0] = paged_decode_stream<DT, D, QR, NS, true, false>;
+  p.main[1][1] = paged_decode_stream<DT, D, QR, NS, true, true>;
+  p.merge[0][0] = paged_decode_stream_merge<DT, D, false, false>;
+  p.merge[0][1] = paged_decode_stream_merge<DT, D, false, true>;
+  p.merge[1][0] = paged_decode_stream_merge<DT, D, true, false>;
+  p.merge[1][1] = paged_decode_stream_merge<DT, D, true, true>;
   p.ring_bytes = NS * Ring<D, QR>::STAGE;
   return p;
 }
@@ -689,14 +846,14 @@ StreamConfig stream_config(int dtype, int d, int group, int batch) {
   StreamConfig c{};
   if (batch < 1 || batch > kStreamMaxBatch || group < 1 || group > 16) return c;
   const StreamPick p = pick(dtype, d, group);
-  if (!p.main) return c;
+  if (!p.main[0][0]) return c;
   const int scan_bytes = (2 * batch + 1 + kSW) * 4;
   const int ring_bytes = kSW * p.ring_bytes;
   c.lds_bytes = scan_bytes > ring_bytes ? scan_bytes : ring_bytes;
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess) return c;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return c;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(p.main), kSW * kWave,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(p.main[0][0]), kSW * kWave,
                                                    c.lds_bytes) != hipSuccess)
     return c;
   c.grid = cus * (per_cu > 0 ? per_cu : 1);
@@ -713,9 +870,34 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, i
   sa.tw = cfg.tw;
   sa.min_tiles = stream_min_tiles();
   sa.rec_stride = static_cast<int>(cfg.rec_floats);
-  const bool fused = sa.app.slots != nullptr;
-  hipLaunchKernelGGL(fused ? p.main_fused : p.main, dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
-  hipLaunchKernelGGL(fused ? p.merge_fused : p.merge, dim3(num_kv_heads, batch), dim3(256), 0, stream, sa);
+  const int fused = sa.app.slots != nullptr, planned = sa.plan != nullptr;
+  hipLaunchKernelGGL(p.main[fused][planned], dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
+  hipLaunchKernelGGL(p.merge[fused][planned], dim3(num_kv_heads, batch), dim3(256), 0, stream, sa);
+  return static_cast<int>(hipGetLastError());
+}
+
+int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads) {
+  return (kPlanHeader + static_cast<int64_t>(cfg.tw) * kPlanWave +
+          static_cast<int64_t>(batch) * num_kv_heads * kPlanSeg) * 4;
+}
+
+int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32_t* block_tables, int64_t bt_stride,
+                       int batch, int num_kv_heads, int block_size, int max_blocks, int32_t* plan,
+                       hipStream_t stream) {
+  PlanArgs p{};
+  p.lens = lens;
+  p.bt = block_tables;
+  p.bt_stride = bt_stride;
+  p.plan = plan;
+  p.batch = batch;
+  p.hkv = num_kv_heads;
+  p.bs = block_size;
+  p.log2_bs = ilog2_exact(block_size);
+  p.cap = max_blocks * block_size;
+  p.tw = cfg.tw;
+  p.min_tiles = stream_min_tiles();
+  const size_t lds = static_cast<size_t>(2 * batch + 1 + kPlanThreads / kWave) * 4;
+  hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), lds, stream, p);
   return static_cast<int>(hipGetLastError());
 }
 

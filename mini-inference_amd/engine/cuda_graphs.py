@@ -54,6 +54,13 @@ class _GraphDecodeContext:
         self.slot_mapping = owner.slot_mapping[:batch]
         self.context_lens = owner.context_lens[:batch]
         self.scale = 1.0 / (owner.cache.head_dim ** 0.5)
+        self.num_heads = owner.model.cfg.num_heads
+        # Buffer of the step's work plan; prepare() fills it inside the graph. (The launch is
+        # issued there, not prepared here, so that it binds the capturing stream.)
+        self.plan = paged_ops.prepare_decode_plan(self.context_lens, self.tables, self.num_heads,
+                                                  owner.cache.num_kv_heads, owner.cache.head_dim,
+                                                  owner.cache.block_size, owner.cache.k.dtype,
+                                                  max_blocks=self.num_blocks)[1]
 
     def prepare(self) -> None:
         """Inside the graph, once per step: slot mapping and context lengths from the static buffers."""
@@ -61,12 +68,16 @@ class _GraphDecodeContext:
         write_blocks = self.tables.gather(1, torch.div(self.positions, bs, rounding_mode="floor").unsqueeze(1))
         self.slot_mapping.copy_(write_blocks.squeeze(1).to(torch.int64) * bs + self.positions % bs)
         self.context_lens.copy_(self.positions + 1)
+        if self.plan is not None:
+            c = self.cache
+            paged_ops.decode_plan(self.context_lens, self.tables, self.num_heads, c.num_kv_heads, c.head_dim,
+                                  c.block_size, c.k.dtype, max_blocks=self.num_blocks, plan=self.plan)
 
     def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
         out = paged_ops.paged_decode_append(q[:, :, 0], k[:, :, 0], v[:, :, 0], k_layer, v_layer, self.slot_mapping,
                                             self.tables, self.context_lens, scale=self.scale,
-                                            max_blocks=self.num_blocks)
+                                            max_blocks=self.num_blocks, plan=self.plan)
         return out.unsqueeze(2)
 
 

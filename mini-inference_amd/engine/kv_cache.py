@@ -303,6 +303,7 @@ class PagedDecodeContext:
         self.kv_len = nb * bs
         self.scale = 1.0 / (cache.head_dim ** 0.5)
         self._mask: torch.Tensor | None = None
+        self._plan: tuple[tuple, torch.Tensor | None] | None = None  # (shape key, work plan)
 
     @property
     def tables(self) -> torch.Tensor:
@@ -317,12 +318,22 @@ class PagedDecodeContext:
             self._mask = (keys <= self.positions.unsqueeze(1))[:, None, None, :]
         return self._mask
 
+    def plan(self, num_heads: int, dtype: torch.dtype) -> torch.Tensor | None:
+        """The step's decode work plan (made by the first layer's call, shared by the rest)."""
+        key = (num_heads, dtype)
+        if self._plan is None or self._plan[0] != key:
+            c = self.cache
+            p = paged_ops.decode_plan(self.context_lens, self.block_tables, num_heads, c.num_kv_heads, c.head_dim,
+                                      c.block_size, dtype, max_blocks=self.num_blocks)
+            self._plan = (key, p)
+        return self._plan[1]
+
     def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         """Append this step's k/v and attend (engine/kv_cache.py:611-620) in one fused call."""
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
         out = paged_ops.paged_decode_append(q[:, :, 0], k[:, :, 0], v[:, :, 0], k_layer, v_layer, self.slot_mapping,
                                             self.block_tables, self.context_lens, scale=self.scale,
-                                            max_blocks=self.num_blocks)
+                                            max_blocks=self.num_blocks, plan=self.plan(q.shape[1], q.dtype))
         return out.unsqueeze(2)
 
     def commit(self) -> None:

@@ -40,8 +40,10 @@ class PreparedCall:
     """One validated C-ABI call with its argument tuple fixed (pointers, strides, stream).
 
     Calling it re-launches the kernel on the same buffers with no Python-side checks, for
-    loops over static buffers (graph capture, timing). The tensors passed to the
-    ``prepare_*`` function must stay alive and in place while it is used.
+    loops over static buffers (timing, serving loops). The stream is the one current when
+    the call was prepared: a call meant for a graph must be prepared inside the capture.
+    The tensors passed to the ``prepare_*`` function must stay alive and in place while it
+    is used.
     """
 
     __slots__ = ("_fn", "_args", "_what", "keep")
@@ -134,11 +136,13 @@ def decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_d
 def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                          context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
                          max_blocks: int | None = None, workspace: torch.Tensor | None = None,
-                         append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None):
+                         append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+                         plan: torch.Tensor | None = None):
     """Validate a :func:`paged_decode` call once; returns ``(PreparedCall, out)``.
 
     ``append = (k, v, slot_mapping)`` prepares the fused append + decode call
-    (:func:`paged_decode_append`) instead.
+    (:func:`paged_decode_append`) instead. ``plan`` is a work plan from :func:`decode_plan`
+    for the same context lengths and block tables (or None).
     """
     _require_device(q, k_cache, v_cache, block_tables, context_lens)
     if q.dim() != 3 or q.stride(2) != 1:
@@ -176,10 +180,16 @@ def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
         raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, needs {need}")
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    if plan is not None:
+        _require_device(plan)
+        if plan.dtype != torch.int32 or not plan.is_contiguous():
+            raise ValueError("plan must be a contiguous int32 tensor from decode_plan")
+    plan_ptr = plan.data_ptr() if plan is not None else None
     args = (out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1),
             k_cache.data_ptr(), v_cache.data_ptr(), nb, block_tables.data_ptr(), block_tables.stride(0),
-            context_lens.data_ptr(), b, hq, hkv, d, bs, mb, scale, ws_ptr, ws_bytes, code, _stream_ptr(q.device))
-    keep = (out, q, k_cache, v_cache, block_tables, context_lens, workspace)
+            context_lens.data_ptr(), b, hq, hkv, d, bs, mb, scale, ws_ptr, ws_bytes, plan_ptr, code,
+            _stream_ptr(q.device))
+    keep = (out, q, k_cache, v_cache, block_tables, context_lens, workspace, plan)
     if append is None:
         return PreparedCall(lib.mip_paged_decode, args, "mip_paged_decode", keep), out
     k, v, slot_mapping = append
@@ -197,9 +207,52 @@ def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
     return PreparedCall(lib.mip_paged_decode_append, fused, "mip_paged_decode_append", keep + (k, v, slot_mapping)), out
 
 
+def prepare_decode_plan(context_lens: torch.Tensor, block_tables: torch.Tensor, num_heads: int, num_kv_heads: int,
+                        head_dim: int, block_size: int, dtype: torch.dtype, max_blocks: int | None = None,
+                        plan: torch.Tensor | None = None):
+    """A prepared :func:`decode_plan` launch and its plan tensor, or ``(None, None)`` where the
+    stream kernel does not run (then decode calls take no plan)."""
+    _require_device(context_lens, block_tables)
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.stride(1) != 1:
+        raise ValueError("block_tables must be int32 [B, max_blocks] with contiguous rows")
+    b = block_tables.shape[0]
+    if context_lens.dtype != torch.int32 or context_lens.shape != (b,) or not context_lens.is_contiguous():
+        raise ValueError("context_lens must be contiguous int32 [B]")
+    mb = block_tables.shape[1] if max_blocks is None else int(max_blocks)
+    code = dtype_code(dtype)
+    lib = _native.load()
+    need = int(lib.mip_paged_decode_plan_bytes(b, num_heads, num_kv_heads, head_dim, block_size, mb, code))
+    if need == 0:
+        return None, None
+    if plan is None:
+        plan = torch.empty(-(-need // 4), dtype=torch.int32, device=context_lens.device)
+    elif plan.dtype != torch.int32 or not plan.is_contiguous() or plan.numel() * 4 < need:
+        raise ValueError(f"plan must be a contiguous int32 tensor of at least {need} bytes")
+    args = (context_lens.data_ptr(), block_tables.data_ptr(), block_tables.stride(0), b, num_heads, num_kv_heads,
+            head_dim, block_size, mb, code, plan.data_ptr(), plan.numel() * 4, _stream_ptr(context_lens.device))
+    keep = (context_lens, block_tables, plan)
+    return PreparedCall(lib.mip_paged_decode_plan, args, "mip_paged_decode_plan", keep), plan
+
+
+def decode_plan(context_lens: torch.Tensor, block_tables: torch.Tensor, num_heads: int, num_kv_heads: int,
+                head_dim: int, block_size: int, dtype: torch.dtype, max_blocks: int | None = None,
+                plan: torch.Tensor | None = None) -> torch.Tensor | None:
+    """One decode step's work plan for the stream kernel (None where that kernel does not run).
+
+    Every layer's :func:`paged_decode` / :func:`paged_decode_append` with these context
+    lengths and tables can take it and skip deriving the work split.
+    """
+    call, plan = prepare_decode_plan(context_lens, block_tables, num_heads, num_kv_heads, head_dim, block_size,
+                                     dtype, max_blocks, plan)
+    if call is not None:
+        call()
+    return plan
+
+
 def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                  context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
-                 max_blocks: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                 max_blocks: int | None = None, workspace: torch.Tensor | None = None,
+                 plan: torch.Tensor | None = None) -> torch.Tensor:
     """Decode attention over paged K/V for one query token per sequence.
 
     ``q``: ``[B, Hq, D]`` (last dim contiguous). ``k_cache``/``v_cache``: one layer,
@@ -209,7 +262,7 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     engine/model.py:126-147 with ``scale = 1/sqrt(D)`` by default.
     """
     call, out = prepare_paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, out, max_blocks,
-                                     workspace)
+                                     workspace, plan=plan)
     call()
     return out
 
@@ -217,14 +270,15 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
 def paged_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
                         v_cache: torch.Tensor, slot_mapping: torch.Tensor, block_tables: torch.Tensor,
                         context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
-                        max_blocks: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                        max_blocks: int | None = None, workspace: torch.Tensor | None = None,
+                        plan: torch.Tensor | None = None) -> torch.Tensor:
     """:func:`kv_append` of the step's ``k``/``v`` ``[B, Hkv, D]`` at ``slot_mapping``, then
     :func:`paged_decode`, as one call (engine/kv_cache.py:611-620). One kernel launch on the
     stream-kernel path; ``slot_mapping[b]`` must be the slot of key ``context_lens[b] - 1``
     (or outside the pool).
     """
     call, out = prepare_paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, out, max_blocks,
-                                     workspace, append=(k, v, slot_mapping))
+                                     workspace, append=(k, v, slot_mapping), plan=plan)
     call()
     return out
 

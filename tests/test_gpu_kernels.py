@@ -285,6 +285,86 @@ def test_fused_append_decode_equals_two_calls(gpu, dtype, d, hq, hkv, bs, algo):
     assert attention_error(values(out_b), want, dtype) <= TOL[dtype]
 
 
+def _plan_restated(plan: np.ndarray, lens, tables, hkv, bs, cap):
+    """Host restatement of the work plan's fields from its header (T, W): ranges, cursors,
+    block-id hints and segment descriptors, as the stream kernel derives them."""
+    L = [min(max(n, 0), cap) for n in lens]
+    tiles = [(n + 15) // 16 for n in L]
+    pre = np.concatenate([[0], np.cumsum(tiles)]).astype(np.int64)
+    T, W = int(plan[0]), int(plan[1])
+    assert T == hkv * pre[-1] and plan[2] == len(lens) and plan[3] == hkv
+    assert (T == 0) == (W == 0) and W <= T
+    for g in range(W):
+        r = plan[8 + 16 * g: 8 + 16 * (g + 1)]
+        lo, hi = g * T // W, (g + 1) * T // W
+        b = max(i for i in range(len(lens)) if hkv * pre[i] <= lo and tiles[i] > 0)
+        rem = lo - hkv * pre[b]
+        kvh, t = rem // tiles[b], rem % tiles[b]
+        assert list(r[:6]) == [lo, hi, b, kvh, t, L[b]], (g, list(r[:6]))
+        if bs >= 16:
+            assert r[6] == 2
+            hints, cb, ck, ct = [], b, kvh, t
+            for k in range(2):
+                if k > 0 and lo + k < hi:
+                    ct += 1
+                    if ct >= tiles[cb]:
+                        ct, ck = 0, ck + 1
+                        if ck >= hkv:
+                            ck, cb = 0, cb + 1
+                            while tiles[cb] == 0:
+                                cb += 1
+                hints.append(tables[cb][16 * ct // bs])
+            assert list(r[7:9]) == hints
+        else:
+            assert r[6] == 0
+    seg = plan[8 + 16 * W:]
+    for b in range(len(lens)):
+        for kvh in range(hkv):
+            r = seg[4 * (b * hkv + kvh): 4 * (b * hkv + kvh) + 4]
+            if tiles[b] == 0:
+                assert list(r) == [0, 0, 0, L[b]]
+                continue
+            s0 = hkv * pre[b] + kvh * tiles[b]
+            e1 = s0 + tiles[b] - 1
+            g_lo, g_hi = ((s0 + 1) * W - 1) // T, ((e1 + 1) * W - 1) // T
+            assert list(r) == [g_lo, g_hi - g_lo + 1, int(g_lo * T // W < s0), L[b]]
+
+
+@pytest.mark.parametrize("dtype,d,hq,hkv,bs", [("bfloat16", 64, 14, 2, 16), ("float16", 128, 28, 4, 32),
+                                               ("bfloat16", 64, 14, 2, 4), ("bfloat16", 128, 16, 1, 8)])
+def test_decode_plan(gpu, dtype, d, hq, hkv, bs):
+    """The per-step work plan: its contents vs the host restatement; decode and fused calls
+    with the plan bit-identical to the same calls deriving the split in-kernel."""
+    from engine import paged_ops
+
+    announce(f"decode plan {dtype} d={d} hq={hq} hkv={hkv} bs={bs}")
+    lens = [1, bs, bs + 1, 37, 513, 1200, 2049, 5, 0, 64, 17, 3000]
+    batch = len(lens)
+    q, k_pool, v_pool, tables, bt, width = _random_case(dtype, batch, hq, hkv, d, bs, lens, seed=5 * d + bs)
+    bt_t = torch.from_numpy(bt).to(gpu)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=gpu)
+    plan = paged_ops.decode_plan(lens_t, bt_t, hq, hkv, d, bs, DTYPES[dtype], max_blocks=width)
+    assert plan is not None
+    torch.cuda.synchronize()
+    _plan_restated(plan.cpu().numpy(), lens, tables, hkv, bs, width * bs)
+    qg, kg, vg = q.to(gpu), k_pool.to(gpu), v_pool.to(gpu)
+    out0 = paged_ops.paged_decode(qg, kg, vg, bt_t, lens_t, max_blocks=width)
+    out1 = paged_ops.paged_decode(qg, kg, vg, bt_t, lens_t, max_blocks=width, plan=plan)
+    torch.cuda.synchronize()
+    assert torch.equal(out0, out1)
+    # fused append + decode with the plan vs without
+    g = torch.Generator().manual_seed(3)
+    k_new = torch.randn(batch, hkv, d, generator=g).to(DTYPES[dtype]).to(gpu)
+    v_new = torch.randn(batch, hkv, d, generator=g).to(DTYPES[dtype]).to(gpu)
+    slots = torch.tensor([tables[b][(n - 1) // bs] * bs + (n - 1) % bs if n > 0 else -1 for b, n in enumerate(lens)],
+                         dtype=torch.int64, device=gpu)
+    ka, va, kb, vb = kg.clone(), vg.clone(), kg.clone(), vg.clone()
+    fa = paged_ops.paged_decode_append(qg, k_new, v_new, ka, va, slots, bt_t, lens_t, max_blocks=width)
+    fb = paged_ops.paged_decode_append(qg, k_new, v_new, kb, vb, slots, bt_t, lens_t, max_blocks=width, plan=plan)
+    torch.cuda.synchronize()
+    assert torch.equal(fa, fb) and torch.equal(ka, kb) and torch.equal(va, vb)
+
+
 def test_paged_decode_large_logits_rescale(gpu):
     """Scores spanning hundreds of units exercise the lazy running-max rescale."""
     from engine import paged_ops
