@@ -365,6 +365,28 @@ def test_decode_plan(gpu, dtype, d, hq, hkv, bs):
     assert torch.equal(fa, fb) and torch.equal(ka, kb) and torch.equal(va, vb)
 
 
+def test_paged_decode_edge_batches(gpu):
+    """A batch above the stream kernel's limit (falls back to the partition kernel), one long
+    sequence (32k keys, many pieces per segment), and lengths beyond max_blocks * block_size
+    (clamped, per the ABI)."""
+    from engine import paged_ops
+
+    announce("paged_decode B=4100 short contexts")
+    lens = [(i * 37) % 60 + 1 for i in range(4100)]
+    _check_decode(gpu, "bfloat16", len(lens), 14, 2, 64, 16, lens, seed=21)
+    announce("paged_decode B=1 ctx 32768")
+    _check_decode(gpu, "bfloat16", 1, 14, 2, 64, 16, [32768], seed=22)
+    announce("paged_decode clamped context lengths")
+    lens = [40, 100, 64]
+    q, k_pool, v_pool, tables, bt, width = _random_case("float16", 3, 8, 2, 64, 16, lens, seed=23)
+    mb = 3  # 48 keys: the first two sequences are clamped to 48
+    out = paged_ops.paged_decode(q.to(gpu), k_pool.to(gpu), v_pool.to(gpu), torch.from_numpy(bt).to(gpu),
+                                 torch.tensor(lens, dtype=torch.int32, device=gpu), max_blocks=mb)
+    torch.cuda.synchronize()
+    want = ref.attention_f64(values(q), values(k_pool), values(v_pool), tables, [min(n, 48) for n in lens], 16)
+    assert attention_error(values(out), want, "float16") <= TOL["float16"]
+
+
 def test_paged_decode_large_logits_rescale(gpu):
     """Scores spanning hundreds of units exercise the lazy running-max rescale."""
     from engine import paged_ops
