@@ -75,6 +75,38 @@ int mip_kv_append(const void* k_src, const void* v_src,
                   int32_t dtype, void* stream);
 
 /*
+ * Rotary position embedding of q and k, fused with the KV append.
+ *
+ * Replaces, in one launch, the rotation of one decoder layer
+ *   engine/model.py:249          q, k = apply_rope(q, k, cos, sin)
+ *   engine/model.py:216-224      x * cos + _rotate_half(x) * sin,  _rotate_half(x) = cat(-x2, x1)
+ * and the scatter that follows it in the cache context (engine/kv_cache.py:613-614 decode,
+ * :286-289 packed prefill).
+ *
+ * Token i, element j of a head row x (d = head_dim / 2, c = cos row i, s = sin row i):
+ *     x'[j]     = rnd(rnd(x[j] * c[j])         + rnd(-x[j + d] * s[j]))       j < d
+ *     x'[j + d] = rnd(rnd(x[j + d] * c[j + d]) + rnd(x[j] * s[j + d]))
+ * with products and sums in fp32 and rnd = round to nearest even into dtype (identity for
+ * fp32): exactly the values torch's op-by-op evaluation stores, so the results are
+ * bit-identical to apply_rope in dtype. The q rows (num_heads per token) and k rows
+ * (num_kv_heads per token) are rotated IN PLACE. The rotated k rows and the v rows are
+ * then written to the pool as mip_kv_append does: slot = slot_mapping[i], slots outside
+ * [0, num_cache_blocks * block_size) are skipped (no pool write; q and k are still rotated).
+ *
+ * cos/sin: one row of head_dim elements of dtype per token, row i at cos + i * cs_stride_tok
+ * (the [B, 1, T, D] tables of engine/model.py:211-213, token i = b * T + t). q may be NULL
+ * when num_heads is 0. head_dim must be even.
+ */
+int mip_rope_kv_append(void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                       void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                       const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                       const void* cos, const void* sin, int64_t cs_stride_tok,
+                       void* k_cache, void* v_cache, int64_t num_cache_blocks,
+                       const int64_t* slot_mapping, int32_t n_tokens, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                       int32_t dtype, void* stream);
+
+/*
  * Paged decode attention (one new token per sequence, GQA).
  *
  * Replaces the gather + SDPA of PagedDecodeContext.attend

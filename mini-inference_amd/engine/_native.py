@@ -19,6 +19,7 @@ EXPORTED = (
     "mip_version",
     "mip_status_string",
     "mip_kv_append",
+    "mip_rope_kv_append",
     "mip_paged_decode",
     "mip_paged_decode_append",
     "mip_paged_decode_workspace",
@@ -36,6 +37,11 @@ _SIGNATURES = {
     "mip_kv_append": (
         _c.c_int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "mip_rope_kv_append": (
+        _c.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
+         _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "mip_paged_decode": (
         _c.c_int,

@@ -55,6 +55,7 @@ class _GraphDecodeContext:
         self.context_lens = owner.context_lens[:batch]
         self.scale = 1.0 / (owner.cache.head_dim ** 0.5)
         self.num_heads = owner.model.cfg.num_heads
+        self.fuse_rope = owner.fuse_rope
         # Buffer of the step's work plan; prepare() fills it inside the graph. (The launch is
         # issued there, not prepared here, so that it binds the capturing stream.)
         self.plan = paged_ops.prepare_decode_plan(self.context_lens, self.tables, self.num_heads,
@@ -80,6 +81,17 @@ class _GraphDecodeContext:
                                             max_blocks=self.num_blocks, plan=self.plan)
         return out.unsqueeze(2)
 
+    def attend_rope(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                    sin: torch.Tensor) -> torch.Tensor:
+        """Rotary embedding fused with the append, then the decode kernel (as ``PagedDecodeContext``)."""
+        k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
+        q1 = q[:, :, 0]
+        paged_ops.rope_kv_append(q1, k[:, :, 0], v[:, :, 0], cos[:, 0, 0], sin[:, 0, 0], k_layer, v_layer,
+                                 self.slot_mapping)
+        out = paged_ops.paged_decode(q1, k_layer, v_layer, self.tables, self.context_lens, scale=self.scale,
+                                     max_blocks=self.num_blocks, plan=self.plan)
+        return out.unsqueeze(2)
+
 
 class GraphedDecoder:
     """Captures the decode step as HIP graphs and replays them (engine/cuda_graphs.py:95-189).
@@ -88,10 +100,12 @@ class GraphedDecoder:
     when no captured graph fits, and the caller runs the eager step instead.
     """
 
-    def __init__(self, model: Qwen2ForCausalLM, cache: PagedKVCache, max_batch: int, kv_step: int | None = None) -> None:
+    def __init__(self, model: Qwen2ForCausalLM, cache: PagedKVCache, max_batch: int, kv_step: int | None = None,
+                 fuse_rope: bool = True) -> None:
         if not isinstance(cache, PagedKVCache):
             raise TypeError("GraphedDecoder drives the paged cache")
         self.model, self.cache = model, cache
+        self.fuse_rope = fuse_rope  # rotary embedding inside the append kernel (attend_rope)
         self.device = cache.k.device
         self.batch_buckets = _batch_buckets(max_batch)
         self.kv_buckets = _kv_buckets(cache.max_len, kv_step, cache.block_size)

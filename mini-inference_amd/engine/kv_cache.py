@@ -272,7 +272,13 @@ class PagedDecodeContext:
     * ``block_tables`` int32 ``[B, nb]``, rows padded with block 0 like the reference's
       ``tables`` (``nb`` = blocks of the longest sequence);
     * ``context_lens`` int32 ``[B]`` = ``positions + 1`` (keys each query attends).
+
+    With ``fuse_rope`` set (the default) the model hands over q and k before the rotary
+    embedding and calls :meth:`attend_rope`; otherwise it rotates them itself and calls
+    :meth:`attend`, the reference's protocol.
     """
+
+    fuse_rope = True
 
     def __init__(self, cache: PagedKVCache, slots: Sequence[int]) -> None:
         self.cache = cache
@@ -336,6 +342,22 @@ class PagedDecodeContext:
                                             max_blocks=self.num_blocks, plan=self.plan(q.shape[1], q.dtype))
         return out.unsqueeze(2)
 
+    def attend_rope(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                    sin: torch.Tensor) -> torch.Tensor:
+        """``apply_rope`` (engine/model.py:249) + append + attend, on pre-rotation q and k.
+
+        One kernel rotates q and k in place and writes the rotated k and v to the pool; the
+        decode kernel then reads every key, the new one included, from the pool. ``cos`` and
+        ``sin`` are the ``[B, 1, 1, D]`` tables of the step.
+        """
+        k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
+        q1 = q[:, :, 0]
+        paged_ops.rope_kv_append(q1, k[:, :, 0], v[:, :, 0], cos[:, 0, 0], sin[:, 0, 0], k_layer, v_layer,
+                                 self.slot_mapping)
+        out = paged_ops.paged_decode(q1, k_layer, v_layer, self.block_tables, self.context_lens, scale=self.scale,
+                                     max_blocks=self.num_blocks, plan=self.plan(q.shape[1], q.dtype))
+        return out.unsqueeze(2)
+
     def commit(self) -> None:
         for s in self.slots:
             self.cache.lengths[s] += 1
@@ -346,8 +368,11 @@ class PackedPrefillContext:
 
     The scatter of the N packed tokens into the pool is the append kernel. Attention over
     the packed tokens (block-diagonal causal mask, plus read-back of a cached prefix when
-    some sequence already has tokens) is torch SDPA, as in the reference.
+    some sequence already has tokens) is torch SDPA, as in the reference. ``fuse_rope`` as
+    for :class:`PagedDecodeContext`.
     """
+
+    fuse_rope = True
 
     def __init__(self, cache: PagedKVCache, slots: Sequence[int], lengths: Sequence[int]) -> None:
         self.cache = cache
@@ -386,6 +411,21 @@ class PackedPrefillContext:
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
         # k[0] is [Hkv, N, D]; the append kernel takes [N, Hkv, D] views with any strides.
         paged_ops.kv_append(k_layer, v_layer, k[0].transpose(0, 1), v[0].transpose(0, 1), self.slot_mapping)
+        return self._attention(k_layer, v_layer, q, k, v)
+
+    def attend_rope(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                    sin: torch.Tensor) -> torch.Tensor:
+        """``apply_rope`` (engine/model.py:249) + :meth:`attend`, with the rotation fused into the append.
+
+        ``cos``/``sin`` are ``[1, 1, N, D]``; q and k are rotated in place, so the SDPA below
+        sees the same tensors as after ``apply_rope``.
+        """
+        k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
+        paged_ops.rope_kv_append(q[0].transpose(0, 1), k[0].transpose(0, 1), v[0].transpose(0, 1), cos[0, 0],
+                                 sin[0, 0], k_layer, v_layer, self.slot_mapping)
+        return self._attention(k_layer, v_layer, q, k, v)
+
+    def _attention(self, k_layer, v_layer, q, k, v) -> torch.Tensor:
         if self.has_prefix:
             rb, ro = self.read_at
             keys = k_layer[rb, :, ro].transpose(0, 1).unsqueeze(0)

@@ -61,7 +61,12 @@ class Qwen2Config:
 
 
 class AttentionContext(Protocol):
-    """Receives one layer's post-RoPE q, k, v; stores k/v; returns attention output."""
+    """Receives one layer's post-RoPE q, k, v; stores k/v; returns attention output.
+
+    A context whose ``fuse_rope`` attribute is true instead receives q and k before the
+    rotary embedding, with the step's cos/sin tables, through
+    ``attend_rope(layer_idx, q, k, v, cos, sin)``, and applies the rotation itself.
+    """
 
     def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor: ...
 
@@ -126,8 +131,12 @@ class Attention(nn.Module):
         q = q.view(bsz, t, c.num_heads, c.head_dim).transpose(1, 2)
         k = k.view(bsz, t, c.num_kv_heads, c.head_dim).transpose(1, 2)
         v = v.view(bsz, t, c.num_kv_heads, c.head_dim).transpose(1, 2)
-        q, k = apply_rope(q, k, cos, sin)
-        out = ctx.attend(self.layer_idx, q, k, v)  # the call site the cache contexts serve
+        if getattr(ctx, "fuse_rope", False):
+            # The context rotates q and k itself (in place), fused with its KV append.
+            out = ctx.attend_rope(self.layer_idx, q, k, v, cos, sin)
+        else:
+            q, k = apply_rope(q, k, cos, sin)
+            out = ctx.attend(self.layer_idx, q, k, v)  # the call site the cache contexts serve
         return self.o_proj(out.transpose(1, 2).reshape(bsz, t, c.q_size))
 
 

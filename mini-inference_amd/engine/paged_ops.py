@@ -100,6 +100,58 @@ def kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: 
     prepare_kv_append(k_cache, v_cache, k, v, slot_mapping)()
 
 
+def prepare_rope_kv_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                           sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           slot_mapping: torch.Tensor):
+    """Validate a :func:`rope_kv_append` call once; returns a :class:`PreparedCall` (or a no-op for N = 0)."""
+    _require_device(k, v, cos, sin, k_cache, v_cache, slot_mapping)
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache must be contiguous [num_blocks, Hkv, block_size, D] tensors of one shape")
+    nb, hkv, bs, d = k_cache.shape
+    if d % 2:
+        raise ValueError(f"rotary embedding needs an even head_dim, got {d}")
+    if k.dim() != 3 or k.shape != v.shape or k.shape[1:] != (hkv, d):
+        raise ValueError(f"k/v must be [N, {hkv}, {d}], got {tuple(k.shape)} and {tuple(v.shape)}")
+    n = k.shape[0]
+    if q is not None:
+        _require_device(q)
+        if q.dim() != 3 or q.shape[0] != n or q.shape[2] != d or q.stride(2) != 1:
+            raise ValueError(f"q must be [{n}, Hq, {d}] with a contiguous last dimension, got {tuple(q.shape)}")
+    if cos.shape != (n, d) or sin.shape != (n, d) or cos.stride() != sin.stride() or cos.stride(1) != 1:
+        raise ValueError(f"cos/sin must be [{n}, {d}] with one stride and a contiguous last dimension")
+    dt = k_cache.dtype
+    if any(t.dtype != dt for t in (k, v, cos, sin, v_cache) + ((q,) if q is not None else ())):
+        raise TypeError("q, k, v, cos, sin and the cache must share one dtype")
+    if k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("the last (head_dim) dimension of k/v must be contiguous")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or slot_mapping.shape[0] != n:
+        raise ValueError("slot_mapping must be int64 [N]")
+    if not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be contiguous")
+    if n == 0:
+        return _noop
+    lib = _native.load()
+    hq = 0 if q is None else q.shape[1]
+    qp, qs0, qs1 = (None, 0, 0) if q is None else (q.data_ptr(), q.stride(0), q.stride(1))
+    args = (qp, qs0, qs1, k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+            cos.data_ptr(), sin.data_ptr(), cos.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), nb,
+            slot_mapping.data_ptr(), n, hq, hkv, d, bs, dtype_code(dt), _stream_ptr(k_cache.device))
+    return PreparedCall(lib.mip_rope_kv_append, args, "mip_rope_kv_append",
+                        (q, k, v, cos, sin, k_cache, v_cache, slot_mapping))
+
+
+def rope_kv_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                   k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Rotate q and k in place (rotary embedding) and append the rotated k and v to the pool.
+
+    ``q``: ``[N, Hq, D]`` (or None), ``k``/``v``: ``[N, Hkv, D]``, any token/head strides and a
+    contiguous last dimension; ``cos``/``sin``: ``[N, D]`` rows per token. The values equal
+    engine/model.py:216-224 (``x * cos + rotate_half(x) * sin`` evaluated op by op in the
+    dtype) bit for bit, and the pool rows equal :func:`kv_append` of the rotated k and v.
+    """
+    prepare_rope_kv_append(q, k, v, cos, sin, k_cache, v_cache, slot_mapping)()
+
+
 class _Workspace:
     """One scratch buffer per device, grown on demand (no initialisation needed).
 

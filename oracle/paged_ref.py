@@ -10,6 +10,8 @@ Each function restates one piece of the reference (Ham12-3/mini-inference) and c
   decode_inputs        engine/kv_cache.py:592-609   per-step positions / write index / padded tables / mask
   append               engine/kv_cache.py:613-614   k_layer[write_blocks, :, write_offsets] = k[:, :, 0]
                        engine/kv_cache.py:286-289   packed prefill scatter (same indexing, N tokens)
+  rope                 engine/model.py:216-224      x * cos + rotate_half(x) * sin, rounded op by op in the dtype
+  rope_append          engine/model.py:249 + kv_cache.py:613-614   rotate q and k, append the rotated k and v
   gather_kv            engine/kv_cache.py:615-619   k_layer[tables].permute(0, 2, 1, 3, 4).reshape(...)
   decode_attention     engine/model.py:126-147      GQA regroup + SDPA with a [B,1,1,kv_len] bool mask
   sdpa_attention       engine/model.py:101-123      GQA by repeat_interleave + SDPA
@@ -25,7 +27,10 @@ Pinning (tests/test_oracle.py): every function above is checked against the refe
 own known-answer tests restated (tests/test_kv_cache.py:40-46, :120-141, :179-207) and
 against closed forms (L = 1 gives the value row, constant keys give the mean of the values,
 block relabelling and stale padding leave the output unchanged, G = 1 is plain MHA), plus
-planted mistakes that those checks must catch. ``paged_decode_torch`` and ``attention_f64``
+planted mistakes that those checks must catch. ``rope`` is checked against a float64
+complex-number rotation, the angle-0 and quarter-turn special cases, torch's own CPU
+arithmetic in each dtype (the rounding sequence), and planted sign, half-swap and
+rounding mistakes. ``paged_decode_torch`` and ``attention_f64``
 are two independent formulations and are checked against each other.
 """
 
@@ -143,6 +148,42 @@ def append(k_layer: np.ndarray, v_layer: np.ndarray, blocks: np.ndarray, offsets
     """
     k_layer[blocks, :, offsets] = k_rows
     v_layer[blocks, :, offsets] = v_rows
+
+
+# --------------------------------------------------------------------------- rotary embedding
+
+
+def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, dtype: str) -> np.ndarray:
+    """``x * cos + _rotate_half(x) * sin`` evaluated op by op in ``dtype`` (engine/model.py:216-224).
+
+    ``_rotate_half(x) = cat(-x[..., D/2:], x[..., :D/2])``. Each torch op on ``dtype``
+    tensors computes in fp32 and rounds its result to ``dtype`` (RNE), so the value stored is
+    ``rnd(rnd(x * cos) + rnd(rotate_half(x) * sin))``. Arrays are storage arrays (float32, or
+    uint16 bit patterns for the 16-bit types); ``cos``/``sin`` broadcast against ``x``.
+    Returns a new storage array.
+    """
+    xf, cf, sf = widen(x, dtype), widen(cos, dtype), widen(sin, dtype)
+    half = xf.shape[-1] // 2
+    rot = np.concatenate([-xf[..., half:], xf[..., :half]], axis=-1)
+    t1 = widen(narrow(xf * cf, dtype), dtype)
+    t2 = widen(narrow(rot * sf, dtype), dtype)
+    return narrow(t1 + t2, dtype)
+
+
+def rope_append(q: np.ndarray, k: np.ndarray, v: np.ndarray, cos: np.ndarray, sin: np.ndarray, dtype: str,
+                k_layer: np.ndarray, v_layer: np.ndarray, slots: np.ndarray, block_size: int):
+    """``apply_rope`` (engine/model.py:249) then the append of the rotated k and v.
+
+    ``q`` ``[N, Hq, D]``, ``k``/``v`` ``[N, Hkv, D]``, ``cos``/``sin`` ``[N, D]``. Slots outside
+    the pool (padding rows) are not written. Returns the rotated ``(q, k)``; the pool is
+    updated in place.
+    """
+    qr = rope(q, cos[:, None, :], sin[:, None, :], dtype)
+    kr = rope(k, cos[:, None, :], sin[:, None, :], dtype)
+    slots = np.asarray(slots, dtype=np.int64)
+    ok = (slots >= 0) & (slots < (k_layer.shape[0] * block_size))
+    append(k_layer, v_layer, slots[ok] // block_size, slots[ok] % block_size, kr[ok], v[ok])
+    return qr, kr
 
 
 def copy_blocks(k_pool: np.ndarray, v_pool: np.ndarray, pairs: Sequence[tuple[int, int]]) -> None:

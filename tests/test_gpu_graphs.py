@@ -43,17 +43,18 @@ def _setup(gpu, lengths, seed=0):
 
 
 @torch.inference_mode()
-def _run(gpu, lengths, batches, exact):
+def _run(gpu, lengths, batches, exact, graph_rope=True, eager_rope=True):
     from engine.cuda_graphs import GraphedDecoder
 
     model, ((ec, eslots), (gc, gslots)) = _setup(gpu, lengths)
     assert eslots == gslots
-    gd = GraphedDecoder(model, gc, max_batch=16)
+    gd = GraphedDecoder(model, gc, max_batch=16, fuse_rope=graph_rope)
     gd.capture(batches=batches)
     tokens = [(7 * i + 3) % 512 for i in range(len(lengths))]
     nb = ec.num_blocks  # the scratch block (index nb) takes the graph's padding rows
     for step in range(4):
         ctx = ec.decode_context(eslots)
+        ctx.fuse_rope = eager_rope
         ids = torch.tensor(tokens, device=gpu).unsqueeze(1)
         want = model.compute_logits(model(ids, ctx.positions.unsqueeze(1), ctx)[:, -1]).float()
         ctx.commit()
@@ -81,3 +82,15 @@ def test_graphed_decode_full_bucket_equals_eager(gpu):
 def test_graphed_decode_padded_bucket(gpu):
     announce("graphed decode, batch 5 in bucket 8 (scratch-block padding rows)")
     _run(gpu, [37, 100, 5, 64, 250], batches=[5], exact=False)
+
+
+def test_graphed_fused_rope_equals_eager_reference_protocol(gpu):
+    """Graph with the rotary embedding inside the append kernel vs the eager step that rotates
+    q and k in torch (``apply_rope``) and calls ``attend``: identical logits and pools."""
+    announce("graphed decode with fused rope vs eager apply_rope + attend, exact")
+    _run(gpu, [37, 100, 5, 64, 250, 17, 128, 300], batches=[8], exact=True, graph_rope=True, eager_rope=False)
+
+
+def test_graphed_unfused_rope_equals_eager(gpu):
+    announce("graphed decode, apply_rope + fused append/decode call, vs eager fused rope, exact")
+    _run(gpu, [37, 100, 5, 64, 250, 17, 128, 300], batches=[8], exact=True, graph_rope=False, eager_rope=True)

@@ -221,6 +221,18 @@ def test_abi_host_checks_return_before_launch(lib):
     assert plan(None, None, 8, 4, 14, 2, 64, 16, 8, _native.MIP_BF16, None, 0, None) == E  # no buffers
     assert plan(None, None, 4, 4, 14, 2, 64, 16, 8, _native.MIP_BF16, None, 0, None) == E  # stride < max_blocks
     assert lib.mip_paged_decode_plan_bytes(0, 14, 2, 64, 16, 8, _native.MIP_BF16) == 0
+    rope = lib.mip_rope_kv_append
+    rargs = [None, 1152, 64, None, 1152, 64, None, 1152, 64, None, None, 64, None, None, 64, None, 0, 14, 2, 64, 16,
+             _native.MIP_BF16, None]
+    assert rope(*rargs) == OK                           # n_tokens = 0
+    odd = list(rargs); odd[19] = 63
+    assert rope(*odd) == E                              # odd head_dim has no rotation pairs
+    nul = list(rargs); nul[16] = 4
+    assert rope(*nul) == E                              # tokens but null pointers
+    dt = list(rargs); dt[21] = 5
+    assert rope(*dt) == E                               # unknown dtype
+    bs = list(rargs); bs[20] = 24
+    assert rope(*bs) == E                               # block size not a power of two
     cp = lib.mip_copy_blocks
     assert cp(None, None, None, 0, 24, 100, 8192, None) == OK
     assert cp(None, None, None, 3, 0, 100, 8192, None) == E
@@ -240,6 +252,9 @@ def test_kernels_refuse_cpu_tensors():
                                torch.ones(1, dtype=torch.int32))
     with pytest.raises(RuntimeError):
         paged_ops.copy_blocks(k[None], v[None], torch.zeros(1, 2, dtype=torch.int64))
+    with pytest.raises(RuntimeError):
+        paged_ops.rope_kv_append(torch.zeros(1, 4, 8), torch.zeros(1, 2, 8), torch.zeros(1, 2, 8), torch.ones(1, 8),
+                                 torch.zeros(1, 8), k, v, torch.zeros(1, dtype=torch.int64))
 
 
 def test_missing_library_raises(tmp_path):
