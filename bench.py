@@ -17,9 +17,9 @@ Reported (one JSON line on stdout):
                 the calls), against the 8 TB/s HBM peak; traffic = measured HBM bytes per call
                 when a counter summary exists under profiles/
   decode_tok_s  B / full decode-step time of a random-init Qwen2.5-0.5B (embedding, 24 layers
-                with GEMMs, RoPE, append, attention, MLP, final norm, logits), the step replayed
-                as one captured HIP graph (engine/cuda_graphs.py); decode_tok_s_eager: the same
-                step launched eagerly
+                with GEMMs, RoPE + append (one fused kernel, mip_rope_kv_append), attention,
+                MLP, final norm, logits), the step replayed as one captured HIP graph
+                (engine/cuda_graphs.py); decode_tok_s_eager: the same step launched eagerly
   cpu_baseline  the reference's torch CPU path (index_put_ append + table gather + SDPA,
                 the oracle's restatement) timed on this host's cores for one layer, fp32
 
@@ -123,8 +123,8 @@ def cpu_baseline(batch, layer_q, layer_k, layer_v, budget_s: float) -> dict:
 def decode_tok_s(batch, steps: int, warmup: int) -> dict:
     """Full random-init Qwen2.5-0.5B decode step at this batch: eager, and replayed as one HIP graph.
 
-    A step = host tables + H2D, embedding, 24 layers (GEMMs, RoPE, KV append, paged
-    attention, MLP), final norm and logits, synchronised. Sequence lengths are restored after
+    A step = host tables + H2D, embedding, 24 layers (GEMMs, RoPE fused with the KV append,
+    paged attention, MLP), final norm and logits, synchronised. Sequence lengths are restored after
     every step, so each step appends at the same positions and attends the same contexts.
     """
     import torch

@@ -82,6 +82,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
     const bool is_q = r < static_cast<uint32_t>(a.hq);
     const bool is_v = r >= static_cast<uint32_t>(a.hq + a.hkv);
     const int h = static_cast<int>(is_q ? r : (is_v ? r - a.hq - a.hkv : r - a.hq));
+    // The slot is loaded first so its latency overlaps the row loads (k and v rows only).
+    const int64_t slot = is_q ? -1 : a.slots[tok];
 
     V lo, hi;
     char* row = nullptr;
@@ -120,9 +122,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
       *reinterpret_cast<V*>(row + lo_off) = lo;
       *reinterpret_cast<V*>(row + hi_off) = hi;
     }
-    if (is_q) continue;
-    const int64_t slot = a.slots[tok];
-    if (slot < 0 || slot >= a.n_slots) continue;  // padding row or invalid slot: no pool write
+    if (slot < 0 || slot >= a.n_slots) continue;  // q row, padding row or invalid slot: no pool write
     const int64_t blk = slot >> a.log2_bs;
     const int64_t off = slot & (a.block_size - 1);
     char* dst = (is_v ? a.v_cache : a.k_cache) + ((blk * a.hkv + h) * a.block_size + off) * a.row_bytes;
