@@ -4,13 +4,19 @@ A decode step launches a few hundred small kernels (24 layers of norms, GEMMs, R
 append and the paged attention); replaying them as one captured graph removes the host
 launch cost. As in the reference:
 
-* inputs live in static device buffers (token ids, positions, block tables) that are
-  overwritten before each replay;
+* inputs live in static device buffers that are overwritten before each replay;
 * one graph per batch bucket (1, 2, 4, 8, then every 16 up to ``max_batch``); rows past
   the real batch point at the cache's scratch block, so their appends land there and their
   outputs are ignored;
 * everything that depends on the inputs (slot mapping, context lengths) is computed inside
   the graph from the static buffers.
+
+Block tables stay on the device (``PagedKVCache.enable_device_tables``). Each step uploads
+only token ids, positions, the batch's sequence ids and the table entries written since the
+previous step, in one copy from a pinned staging row. The graph first writes those entries
+into the device mirror, then gathers the batch's rows from it. The reference instead
+rebuilds and uploads the whole padded ``[B, nb]`` table every step
+(engine/cuda_graphs.py:160-176, engine/kv_cache.py:592-609).
 
 Unlike the reference, the attention kernel reads each sequence's pages in place and its
 launch shape does not depend on the KV length, so one KV bucket (the cache's ``max_len``)
@@ -22,7 +28,6 @@ from __future__ import annotations
 
 from collections.abc import Sequence
 
-import numpy as np
 import torch
 
 from . import paged_ops
@@ -46,6 +51,7 @@ class _GraphDecodeContext:
     """Attention for a captured decode step; reads everything from the static buffers."""
 
     def __init__(self, owner: "GraphedDecoder", batch: int, kv_len: int) -> None:
+        self.owner = owner
         self.cache = owner.cache
         self.batch, self.kv_len = batch, kv_len
         self.num_blocks = kv_len // owner.cache.block_size
@@ -64,7 +70,11 @@ class _GraphDecodeContext:
                                                   max_blocks=self.num_blocks)[1]
 
     def prepare(self) -> None:
-        """Inside the graph, once per step: slot mapping and context lengths from the static buffers."""
+        """Inside the graph, once per step: table updates, the batch's rows, slot mapping, context lengths."""
+        owner = self.owner
+        rows = owner.device_tables.rows
+        rows.view(-1).scatter_(0, owner.journal_flat, owner.journal_block.to(torch.int32))
+        torch.index_select(rows, 0, owner.row_ids[:self.batch], out=owner.tables[:self.batch])
         bs = self.cache.block_size
         write_blocks = self.tables.gather(1, torch.div(self.positions, bs, rounding_mode="floor").unsqueeze(1))
         self.slot_mapping.copy_(write_blocks.squeeze(1).to(torch.int64) * bs + self.positions % bs)
@@ -110,16 +120,30 @@ class GraphedDecoder:
         self.batch_buckets = _batch_buckets(max_batch)
         self.kv_buckets = _kv_buckets(cache.max_len, kv_step, cache.block_size)
         top = self.batch_buckets[-1]
-        max_blocks = self.kv_buckets[-1] // cache.block_size
+        self.device_tables = cache.enable_device_tables()
+        dt = self.device_tables
+        if self.kv_buckets[-1] // cache.block_size > dt.max_blocks:
+            raise ValueError("KV bucket beyond the cache's max_len")
         dev = self.device
-        self.ids = torch.zeros(top, 1, dtype=torch.long, device=dev)
-        self.positions = torch.zeros(top, dtype=torch.long, device=dev)
-        self.tables = torch.full((top, max_blocks), cache.scratch_block, dtype=torch.int32, device=dev)
+        # Per-step inputs, one int64 buffer: ids | positions | row ids | journal flat index |
+        # journal block. The journal part has a fixed capacity; a step that logs more
+        # applies the excess eagerly before its replay.
+        self.journal_cap = max(64, 2 * top)
+        j = self.journal_cap
+        self._layout = (top, top, top, j, j)
+        n_words = sum(self._layout)
+        self._stage = torch.zeros(n_words, dtype=torch.long, pin_memory=True)
+        self._stage_np = self._stage.numpy()
+        self._inputs = torch.zeros(n_words, dtype=torch.long, device=dev)
+        self.ids = self._inputs[:top].view(top, 1)
+        self.positions = self._inputs[top:2 * top]
+        self.row_ids = self._inputs[2 * top:3 * top]
+        self.journal_flat = self._inputs[3 * top:3 * top + j]
+        self.journal_block = self._inputs[3 * top + j:]
+        self._pad_inputs(0)
+        self.tables = torch.full((top, dt.max_blocks), cache.scratch_block, dtype=torch.int32, device=dev)
         self.slot_mapping = torch.zeros(top, dtype=torch.long, device=dev)
         self.context_lens = torch.ones(top, dtype=torch.int32, device=dev)
-        # Host staging (pinned): ids and positions in one int64 row pair, tables as int32.
-        self._stage_i64 = torch.zeros(2, top, dtype=torch.long, pin_memory=True)
-        self._stage_tables = torch.full((top, max_blocks), cache.scratch_block, dtype=torch.int32, pin_memory=True)
         # (batch, kv_len) -> (graph, its output logits, its context); the context stays alive
         # with the graph because the graph reads its tensors.
         self.graphs: dict[tuple[int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor, _GraphDecodeContext]] = {}
@@ -141,6 +165,16 @@ class GraphedDecoder:
             raise ValueError(f"batch {n} exceeds max_batch {self.batch_buckets[-1]}")
         return b
 
+    def _pad_inputs(self, n: int, n_journal: int = 0) -> None:
+        """Staging rows from ``n`` (and journal entries from ``n_journal``) on: padding values."""
+        top, j = self.batch_buckets[-1], self.journal_cap
+        st, dt = self._stage_np, self.device_tables
+        st[n:top] = 0
+        st[top + n:2 * top] = 0
+        st[2 * top + n:3 * top] = dt.spare_row
+        st[3 * top + n_journal:3 * top + j] = dt.spare_row * dt.max_blocks
+        st[3 * top + j + n_journal:] = self.cache.scratch_block
+
     def _capture_one(self, batch: int, kv_len: int) -> None:
         ctx = _GraphDecodeContext(self, batch, kv_len)
 
@@ -149,9 +183,10 @@ class GraphedDecoder:
             hidden = self.model(self.ids[:batch], self.positions[:batch].unsqueeze(1), ctx)
             return self.model.compute_logits(hidden[:, -1]).float()
 
-        # Every row points at the scratch block while recording.
-        self.positions.zero_()
-        self.tables.fill_(self.cache.scratch_block)
+        # Every row points at the spare (all-scratch) table row while recording.
+        self._pad_inputs(0)
+        self._inputs.copy_(self._stage)
+        self.device_tables.sync()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):  # warm-up outside the graph: kernel selection, workspace, allocator
@@ -177,20 +212,19 @@ class GraphedDecoder:
             raise ValueError("a sequence has no block for its next token (call ensure_capacity first)")
         self.cache.prepare_writes(list(slots), positions, [1] * n)  # copy-on-write of shared blocks
         graph, logits, _ = self.graphs[(batch, kv_len)]
-        nb = kv_len // bs
-        st, tb = self._stage_i64, self._stage_tables
-        st[0, :n] = torch.as_tensor(list(last_tokens), dtype=torch.long)
-        st[0, n:batch] = 0
-        st[1, :n] = torch.as_tensor(positions, dtype=torch.long)
-        st[1, n:batch] = 0
-        rows = np.full((batch, nb), self.cache.scratch_block, dtype=np.int32)
-        for i, s in enumerate(slots):
-            row = self.cache.block_tables[s][:nb]
-            rows[i, :len(row)] = row
-        tb[:batch, :nb].copy_(torch.from_numpy(rows))
-        self.ids[:batch, 0].copy_(st[0, :batch], non_blocking=True)
-        self.positions[:batch].copy_(st[1, :batch], non_blocking=True)
-        self.tables[:batch, :nb].copy_(tb[:batch, :nb], non_blocking=True)
+        top, j = self.batch_buckets[-1], self.journal_cap
+        flat, blocks = self.device_tables.flat_entries(self.cache.drain_journal())
+        if len(flat) > j:  # more table changes than the graph's journal holds: the rest now
+            self.device_tables.apply_flat(flat[j:], blocks[j:])
+            flat, blocks = flat[:j], blocks[:j]
+        st, m = self._stage_np, len(flat)
+        st[:n] = last_tokens
+        st[top:top + n] = positions
+        st[2 * top:2 * top + n] = slots
+        st[3 * top:3 * top + m] = flat
+        st[3 * top + j:3 * top + j + m] = blocks
+        self._pad_inputs(n, m)
+        self._inputs.copy_(self._stage, non_blocking=True)
         graph.replay()
         torch.cuda.current_stream().synchronize()  # the pinned staging rows are reused next step
         self.replays += 1

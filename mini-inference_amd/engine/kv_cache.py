@@ -66,6 +66,11 @@ class PagedKVCache:
         self._cached: dict[tuple, int] = {}
         self.prefix_hit_tokens = 0
         self.cow_copies = 0  # blocks copied on write so far
+        self.max_seqs = max_seqs
+        # (slot, index, block) of every table entry written since the last drain; kept only
+        # once a device mirror of the tables exists (enable_device_tables).
+        self._journal: list[tuple[int, int, int]] | None = None
+        self.device_tables: DeviceBlockTables | None = None
 
     @classmethod
     def for_model(cls, cfg: Qwen2Config, num_blocks: int, block_size: int, max_seqs: int, max_len: int,
@@ -141,6 +146,7 @@ class PagedKVCache:
         slot = self._free_ids.pop()
         fresh = [self._new_block() for _ in range(self.blocks_for(num_tokens) - len(shared))]
         self.block_tables[slot] = shared + fresh
+        self._log_table(slot)
         self.lengths[slot] = len(shared) * self.block_size
         self.prefix_hit_tokens += self.lengths[slot]
         return slot
@@ -164,6 +170,8 @@ class PagedKVCache:
             return False
         for _ in range(missing):
             table.append(self._new_block())
+            if self._journal is not None:
+                self._journal.append((slot, len(table) - 1, table[-1]))
         return True
 
     def free(self, slot: int) -> None:
@@ -189,6 +197,7 @@ class PagedKVCache:
         child = self._free_ids.pop()
         self.block_tables[child] = list(table)
         self.lengths[child] = self.lengths[slot]
+        self._log_table(child)
         return child
 
     def ref_count(self, block: int) -> int:
@@ -217,6 +226,8 @@ class PagedKVCache:
                     table[i] = new
                     self._release(old)
                     pairs.append((old, new))
+                    if self._journal is not None:
+                        self._journal.append((slot, i, new))
         if pairs:
             self.copy_blocks(pairs)
             self.cow_copies += len(pairs)
@@ -231,6 +242,34 @@ class PagedKVCache:
                 return
             t = torch.from_numpy(np.asarray(pairs, dtype=np.int64).reshape(-1, 2)).to(self.k.device)
         paged_ops.copy_blocks(self.k, self.v, t)
+
+    # ----------------------------------------------------------------- device-resident tables
+    def _log_table(self, slot: int) -> None:
+        if self._journal is not None:
+            self._journal.extend((slot, i, b) for i, b in enumerate(self.block_tables[slot]))
+
+    def enable_device_tables(self) -> "DeviceBlockTables":
+        """Keep a device mirror of every block table, updated from a journal of changes.
+
+        The reference rebuilds the padded ``[B, nb]`` tables on the host and copies them to
+        the device every step (engine/kv_cache.py:592-609). With the mirror, only the
+        entries written since the last step travel (a new block every ``block_size`` tokens
+        per sequence, copy-on-write replacements, new sequences).
+        """
+        if self.device_tables is None:
+            self._journal = []
+            for slot in self.block_tables:
+                self._log_table(slot)
+            self.device_tables = DeviceBlockTables(self)
+        return self.device_tables
+
+    def drain_journal(self) -> np.ndarray:
+        """int64 ``[n, 3]`` rows ``(slot, index, block)`` logged since the last drain, oldest first."""
+        if not self._journal:
+            return np.zeros((0, 3), dtype=np.int64)
+        out = np.asarray(self._journal, dtype=np.int64)
+        self._journal.clear()
+        return out
 
     # ----------------------------------------------------------------- index helpers
     def write_index(self, slots: Sequence[int], starts: Sequence[int],
@@ -260,6 +299,48 @@ class PagedKVCache:
 
     def decode_context(self, slots: Sequence[int]) -> "PagedDecodeContext":
         return PagedDecodeContext(self, slots)
+
+
+class DeviceBlockTables:
+    """Device mirror of a cache's block tables: int32 ``rows [max_seqs + 1, max_blocks]``.
+
+    Row ``slot`` holds that sequence's table; entries past its length are stale and never
+    read (every kernel stops at the sequence's context length). The last row, ``spare_row``,
+    only ever holds the scratch block: padding rows of a batch point at it, and unused
+    entries of a fixed-size journal write into it.
+    """
+
+    def __init__(self, cache: PagedKVCache) -> None:
+        self.cache = cache
+        self.max_blocks = cache.blocks_for(cache.max_len)
+        self.spare_row = cache.max_seqs
+        self.rows = torch.full((cache.max_seqs + 1, self.max_blocks), cache.scratch_block, dtype=torch.int32,
+                               device=cache.k.device)
+
+    def flat_entries(self, journal: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+        """Distinct (flat index into ``rows``, block) pairs of a journal, the newest entry winning.
+
+        A scatter with repeated indices leaves an unspecified winner, so an entry written
+        twice (a slot freed and reused, a block replaced by copy-on-write) keeps only its last
+        value here.
+        """
+        flat = journal[:, 0] * self.max_blocks + journal[:, 1]
+        _, last = np.unique(flat[::-1], return_index=True)
+        keep = len(flat) - 1 - last
+        return flat[keep], journal[keep, 2]
+
+    def apply_flat(self, flat: np.ndarray, blocks: np.ndarray) -> None:
+        """Scatter distinct ``rows.view(-1)[flat] = blocks`` now, on the current stream."""
+        if len(flat) == 0:
+            return
+        both = torch.from_numpy(np.concatenate([flat, blocks]).astype(np.int64)).to(self.rows.device)
+        n = len(flat)
+        self.rows.view(-1).scatter_(0, both[:n], both[n:].to(torch.int32))
+
+    def sync(self) -> None:
+        """Apply everything the cache logged since the last drain."""
+        self.apply_flat(*self.flat_entries(self.cache.drain_journal()))
+
 
 
 class PagedDecodeContext:

@@ -94,3 +94,47 @@ def test_graphed_fused_rope_equals_eager_reference_protocol(gpu):
 def test_graphed_unfused_rope_equals_eager(gpu):
     announce("graphed decode, apply_rope + fused append/decode call, vs eager fused rope, exact")
     _run(gpu, [37, 100, 5, 64, 250, 17, 128, 300], batches=[8], exact=True, graph_rope=False, eager_rope=True)
+
+
+@torch.inference_mode()
+def test_graphed_decode_device_tables_follow_growth_fork_and_reuse(gpu):
+    """40 steps over 8 sequences that cross block boundaries (new blocks every 16 tokens), with
+    a sequence freed and its slot reused at step 12 and a fork (copy-on-write on its first
+    write) at step 24. The graph reads the device-resident tables, updated only through the
+    cache's journal; the eager step rebuilds them on the host. Logits and pools must match."""
+    from engine.cuda_graphs import GraphedDecoder
+
+    announce("graphed decode, device tables under growth, slot reuse and fork")
+    lengths = [13, 30, 47, 5, 62, 16, 31, 100]
+    model, ((ec, eslots), (gc, gslots)) = _setup(gpu, lengths)
+    gd = GraphedDecoder(model, gc, max_batch=8)
+    gd.capture(batches=[8])
+    tokens = [(5 * i + 1) % 512 for i in range(len(lengths))]
+    for step in range(40):
+        if step == 12:  # free one sequence, start a new one in its slot
+            for c, slots in ((ec, eslots), (gc, gslots)):
+                c.free(slots[3])
+                s = c.allocate(40)
+                c.lengths[s] = 33
+                slots[3] = s
+        if step == 24:  # replace sequence 5 by a fork of sequence 2 (shared partial block)
+            for c, slots in ((ec, eslots), (gc, gslots)):
+                c.free(slots[5])
+                slots[5] = c.fork(slots[2])
+        assert eslots == gslots
+        for c, slots in ((ec, eslots), (gc, gslots)):
+            for s in slots:
+                assert c.ensure_capacity(s, c.lengths[s] + 1)
+        ctx = ec.decode_context(eslots)
+        ids = torch.tensor(tokens, device=gpu).unsqueeze(1)
+        want = model.compute_logits(model(ids, ctx.positions.unsqueeze(1), ctx)[:, -1]).float()
+        ctx.commit()
+        got = gd.decode(gslots, tokens)
+        torch.cuda.synchronize()
+        assert got is not None
+        assert torch.equal(got, want), f"step {step}: graph logits differ from eager"
+        nb = ec.num_blocks
+        assert torch.equal(gc.k[:, :nb], ec.k[:, :nb]) and torch.equal(gc.v[:, :nb], ec.v[:, :nb]), f"step {step}"
+        assert [gc.lengths[s] for s in gslots] == [ec.lengths[s] for s in eslots]
+        tokens = want.argmax(dim=-1).tolist()
+    assert gc.cow_copies == ec.cow_copies >= 1

@@ -147,6 +147,66 @@ def test_fork_copy_on_write_bookkeeping(monkeypatch):
     assert len(copies) == 1
 
 
+def _mirror_matches(cache):
+    rows = cache.device_tables.rows.numpy()
+    for slot, table in cache.block_tables.items():
+        assert rows[slot, :len(table)].tolist() == table, f"slot {slot}"
+    assert (rows[cache.device_tables.spare_row] == cache.scratch_block).all()
+
+
+def test_device_tables_follow_every_table_change(monkeypatch):
+    """The journal replayed into the mirror reproduces every live table after allocate (with
+    prefix hits), ensure_capacity, fork, copy-on-write, free and slot reuse, in any batching
+    of the drains. (The mirror is an ordinary tensor, so this runs on the CPU.)"""
+    import random
+
+    rnd = random.Random(3)
+    cache = tiny_paged(num_blocks=40, block_size=4, max_seqs=6, max_len=48, enable_prefix_caching=True)
+    monkeypatch.setattr(cache, "copy_blocks", lambda pairs: None)
+    prompt = list(range(13))
+    first = cache.allocate(13, prompt)
+    cache.lengths[first] = 13
+    cache.register_prefix(first, prompt)
+    cache.enable_device_tables()  # initial upload of the existing table via the journal
+    cache.device_tables.sync()
+    _mirror_matches(cache)
+    live = [first]
+    for step in range(300):
+        op = rnd.random()
+        if op < 0.25 and cache.num_free_slots and cache.can_allocate(20):
+            s = cache.allocate(rnd.randint(1, 20), prompt if rnd.random() < 0.5 else None)
+            cache.lengths[s] = max(cache.lengths[s], 1)
+            live.append(s)
+        elif op < 0.35 and live and cache.num_free_slots:
+            live.append(cache.fork(rnd.choice(live)))
+        elif op < 0.45 and len(live) > 1:
+            s = live.pop(rnd.randrange(len(live)))
+            cache.free(s)
+        elif live:
+            s = rnd.choice(live)
+            n = cache.lengths[s]
+            if cache.ensure_capacity(s, n + 1):
+                try:
+                    cache.prepare_writes([s], [n], [1])
+                except RuntimeError:
+                    continue
+                cache.lengths[s] = n + 1
+        if rnd.random() < 0.3:  # drains at irregular intervals
+            cache.device_tables.sync()
+            _mirror_matches(cache)
+    cache.device_tables.sync()
+    _mirror_matches(cache)
+
+
+def test_device_table_journal_last_write_wins():
+    cache = tiny_paged(num_blocks=12, block_size=4)
+    dt = cache.enable_device_tables()
+    journal = np.array([[1, 0, 5], [1, 1, 6], [1, 0, 7], [2, 0, 3], [1, 0, 9]], dtype=np.int64)
+    flat, blocks = dt.flat_entries(journal)
+    got = dict(zip(flat.tolist(), blocks.tolist()))
+    assert got == {1 * dt.max_blocks + 0: 9, 1 * dt.max_blocks + 1: 6, 2 * dt.max_blocks: 3}
+
+
 def test_packed_prefill_slot_mapping():
     cache = tiny_paged(num_blocks=12, block_size=4)
     slots = [cache.allocate(0) for _ in range(2)]
