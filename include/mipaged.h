@@ -201,6 +201,38 @@ int mip_paged_decode_plan(const int32_t* context_lens, const int32_t* block_tabl
                           int32_t max_blocks_per_seq, int32_t dtype, void* plan,
                           size_t plan_bytes, void* stream);
 
+/*
+ * Paged varlen prefill attention over a cached prefix.
+ *
+ * Replaces the read-back gather + dense-mask SDPA of PackedPrefillContext.attend
+ *   engine/kv_cache.py:286-294   keys = k_layer[read_0, :, read_2] ...; sdpa_attention(q, keys,
+ *                                 values, attn_mask=self.mask)
+ * with its mask (engine/kv_cache.py:268-276) `key_seg == seg & key_pos <= position`, and, for
+ * sequences with nothing cached, the packed block-diagonal causal SDPA of :290-294.
+ *
+ * Sequence s (0 <= s < num_seqs) owns packed rows r in [cu_q[s], cu_q[s + 1]); row r is its new
+ * token i = r - cu_q[s], at position p = ctx_start[s] + i. For every query head h:
+ *
+ *   out[r, h, :] = softmax_j( scale * q[r, h, :] . K_s[j, :] ) @ V_s[j, :],   0 <= j <= p,
+ *   K_s[j] = k_cache row (block_tables[s * bt_stride + j / block_size], h / group, j % block_size)
+ *
+ * (group = num_heads / num_kv_heads), i.e. each new token sees its sequence's cached prefix
+ * and its own sequence's new tokens up to itself; every key it reads must already be in the
+ * pool (append first). Products and sums in fp32, output rounded once to dtype. Keys past
+ * max_blocks_per_seq * block_size are never read (positions beyond are clamped to the last
+ * one). max_q_len must be >= every cu_q[s + 1] - cu_q[s]; it only sizes the grid, which
+ * depends on the integer arguments alone. Supported: 16-bit dtypes, head_dim 64 or 128,
+ * group <= 16 (else MIP_EUNSUPPORTED); q rows 16-byte aligned, out rows 8-byte aligned.
+ */
+int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                      const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                      const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
+                      const int32_t* block_tables, int64_t bt_stride,
+                      const int32_t* cu_q, const int32_t* ctx_start,
+                      int32_t num_seqs, int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq, float scale,
+                      int32_t dtype, void* stream);
+
 /* Workspace bytes mip_paged_decode and mip_paged_decode_append need for this shape (0 when
  * they need none). */
 size_t mip_paged_decode_workspace(int32_t batch, int32_t num_heads, int32_t num_kv_heads,

@@ -1,0 +1,343 @@
+// Paged varlen prefill attention over a cached prefix (gfx950, MFMA).
+//
+// Reference semantics (engine/kv_cache.py:268-294 PackedPrefillContext with a prefix hit,
+// engine/model.py:101-123 sdpa_attention): several sequences' new tokens are packed end to
+// end; new token i of sequence s sits at position p = ctx_start[s] + i and attends every key
+// 0..p of its own sequence (the cached prefix and the new tokens before it, already appended
+// to the pool). The reference reads all those keys back out of the pool and runs SDPA with a
+// dense [N, total keys] mask; here the keys are read in place through the block table and
+// only each sequence's own causal range is computed. With ctx_start = 0 this is the packed
+// block-diagonal causal prefill of engine/kv_cache.py:290-294.
+//
+// Work split: workgroup (kv head, sequence, block of TQ new tokens), 4 wavefronts. The query
+// rows of a workgroup are (token, head of the kv head's group) pairs: a 16-row column block
+// holds 16 / QR tokens x QR head slots (the group's G heads, padded to QR), and each
+// wavefront owns NC column blocks. Blocks of the same sequence are dispatched latest-first,
+// since later tokens see more keys.
+//
+// Per 32-key tile: all 256 threads copy the K and V rows (found through the block table) into
+// an LDS stage (two stages: the next tile's rows are fetched into registers while the current
+// one is computed); then each wavefront, for each 16-key half:
+//   S^T[16 keys x 16 rows] = K . Q^T      v_mfma_f32_16x16x32, D/32 steps (Q^T in registers)
+//   O^T[D x 16 rows]      += V^T . P^T    v_mfma_f32_16x16x16, D/16 tiles, P split hi + lo
+// with a base-2 online softmax per row, as in the decode kernels. Rows whose position is below
+// a key mask it out; a wavefront skips halves that lie beyond all of its rows' positions.
+#include "paged_decode_common.h"
+
+namespace mip {
+namespace prefill {
+namespace {
+
+using decode::f32x4_t;
+using decode::fast_exp2;
+using decode::kRescaleLog2;
+using decode::MfmaOps;
+
+constexpr int kPW = 4;    // wavefronts per workgroup
+constexpr int kKT = 32;   // keys per LDS tile
+
+struct PrefillArgs {
+  char* out;
+  int64_t out_st, out_sh;  // elements
+  const char* q;
+  int64_t q_st, q_sh;      // elements
+  const char* k;
+  const char* v;
+  int64_t ncb;
+  const int32_t* bt;
+  int64_t bt_stride;
+  const int32_t* cu_q;       // [S + 1] packed row offsets of each sequence's new tokens
+  const int32_t* ctx_start;  // [S] tokens cached before this pass (position of token 0)
+  int hkv, group, bs, log2_bs, max_blocks;
+  float scale_log2;
+};
+
+__device__ __forceinline__ float sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float max4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+template <int D>
+struct PShape {
+  static constexpr int RB = 2 * D;                 // bytes per K / V row
+  static constexpr int CPR = RB / 16;              // 16-byte chunks per row
+  static constexpr int KC = D / 32;                // QK k-steps
+  static constexpr int MT = D / 16;                // PV output tiles
+  static constexpr int TILE = kKT * RB;            // bytes of one K (or V) tile
+  static constexpr int STAGE = 2 * TILE;           // K | V
+  static constexpr int NLD = kKT * CPR / (kPW * kWave);  // 16-byte chunks per thread per tile, each of K and V
+  static_assert(NLD >= 1 && NLD * kPW * kWave == kKT * CPR, "tile must split evenly over the workgroup");
+};
+
+template <int DT, int D, int QR, int NC>
+__global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs a) {
+  using P = PShape<D>;
+  using Ops = MfmaOps<DT>;
+  constexpr int RB = P::RB, CPR = P::CPR, KC = P::KC, MT = P::MT;
+  constexpr int TPC = 16 / QR;                 // tokens per column block
+  constexpr int TQ = kPW * NC * TPC;           // tokens per workgroup
+  __shared__ __attribute__((aligned(16))) char smem[2 * P::STAGE];
+  __shared__ uint8_t s_ok[2][kKT];             // key row holds a real key (valid block id)
+
+  const int kvh = blockIdx.x;
+  const int s = blockIdx.y;
+  const int blk = gridDim.z - 1 - blockIdx.z;  // latest tokens (most keys) first
+  const int q0 = a.cu_q[s];
+  const int n_s = a.cu_q[s + 1] - q0;
+  const int tok_lo = blk * TQ;
+  if (tok_lo >= n_s) return;
+  const int tok_hi = tok_lo + TQ < n_s ? tok_lo + TQ : n_s;
+  const int start = a.ctx_start[s] > 0 ? a.ctx_start[s] : 0;
+  const int cap = a.max_blocks * a.bs;
+  int p_last = start + tok_hi - 1;
+  p_last = p_last < cap - 1 ? p_last : cap - 1;  // keys past the table are never read
+  const int n_tiles = (p_last + kKT) / kKT;
+  const int G = a.group;
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int i16 = lane & 15, grp = lane >> 4;
+  const int32_t* table = a.bt + static_cast<int64_t>(s) * a.bt_stride;
+
+  // ---- this lane's query row in each column block, and its Q^T operand.
+  int pos[NC];
+  bool live[NC];
+  uint4 qreg[NC][KC];
+  int wave_pmax = -1;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int tok = tok_lo + (w * NC + c) * TPC + i16 / QR;
+    const int g = i16 % QR;
+    live[c] = g < G && tok < tok_hi;
+    const int p = start + tok;
+    pos[c] = live[c] ? (p < cap - 1 ? p : cap - 1) : -1;
+    const int last_tok = tok_lo + (w * NC + c) * TPC + TPC - 1;
+    const int wp = start + (last_tok < tok_hi - 1 ? last_tok : tok_hi - 1);
+    wave_pmax = wp > wave_pmax ? wp : wave_pmax;
+    const char* qrow = a.q + ((static_cast<int64_t>(q0) + (live[c] ? tok : 0)) * a.q_st +
+                              static_cast<int64_t>(kvh * G + (live[c] ? g : 0)) * a.q_sh) * 2;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+      qreg[c][kc] = live[c] ? *reinterpret_cast<const uint4*>(qrow + (32 * kc + 8 * grp) * 2) : make_uint4(0, 0, 0, 0);
+  }
+  wave_pmax = __builtin_amdgcn_readfirstlane(wave_pmax < cap - 1 ? wave_pmax : cap - 1);
+
+  // ---- loader: this thread's K / V chunks of a tile.
+  uint4 kbuf[P::NLD], vbuf[P::NLD];
+  bool okbuf[P::NLD];
+  auto fetch = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < P::NLD; ++j) {
+      const int idx = tid + j * kPW * kWave;
+      const int r = idx / CPR, c = idx % CPR;
+      const int key = t * kKT + r;
+      const int kk = key < p_last ? key : p_last;
+      const int b = table[kk >> a.log2_bs];
+      const bool bok = b >= 0 && b < a.ncb;
+      const bool ok = key <= p_last && bok;
+      // Keys past the last position re-read that position's row (a real key, so finite V: the
+      // PV product multiplies every row of the tile, masked or not).
+      const int64_t row = (static_cast<int64_t>(bok ? b : 0) * a.hkv + kvh) * a.bs + (kk & (a.bs - 1));
+      kbuf[j] = *reinterpret_cast<const uint4*>(a.k + row * RB + c * 16);
+      vbuf[j] = *reinterpret_cast<const uint4*>(a.v + row * RB + c * 16);
+      okbuf[j] = ok;
+    }
+  };
+  auto stash = [&](int stage) __attribute__((always_inline)) {
+    char* st = smem + stage * P::STAGE;
+#pragma unroll
+    for (int j = 0; j < P::NLD; ++j) {
+      const int idx = tid + j * kPW * kWave;
+      const int r = idx / CPR, c = idx % CPR;
+      *reinterpret_cast<uint4*>(st + r * RB + ((c ^ (r & (CPR - 1))) * 16)) = kbuf[j];  // K swizzled by row
+      *reinterpret_cast<uint4*>(st + P::TILE + r * RB + c * 16) = vbuf[j];
+      if (c == 0) s_ok[stage][r] = okbuf[j];
+    }
+  };
+
+  f32x4_t acc[NC][MT];
+  float m[NC], l[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    m[c] = -INFINITY;
+    l[c] = 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[c][mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    const int stage = t & 1;
+    if (t + 1 < n_tiles) fetch(t + 1);
+    const char* st = smem + stage * P::STAGE;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int key0 = t * kKT + 16 * u;
+      if (key0 > wave_pmax) break;  // every row of this wavefront sits before these keys
+      uint4 kreg[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const int r = 16 * u + i16, ch = 4 * kc + grp;
+        kreg[kc] = *reinterpret_cast<const uint4*>(st + r * RB + ((ch ^ (r & (CPR - 1))) * 16));
+      }
+      uint32_t vt[MT][2];
+      const uint16_t* vcol = reinterpret_cast<const uint16_t*>(st + P::TILE + (16 * u + 4 * grp) * RB) + i16;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint32_t e0 = vcol[0 * D + 16 * mt], e1 = vcol[1 * D + 16 * mt];
+        const uint32_t e2 = vcol[2 * D + 16 * mt], e3 = vcol[3 * D + 16 * mt];
+        vt[mt][0] = e0 | (e1 << 16);
+        vt[mt][1] = e2 | (e3 << 16);
+      }
+      bool kok[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kok[j] = s_ok[stage][16 * u + 4 * grp + j] != 0;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        f32x4_t sc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) sc = Ops::qk(kreg[kc], qreg[c][kc], sc);
+        float sv[4];
+        bool need = false;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bool ok = kok[j] && key0 + 4 * grp + j <= pos[c];
+          sv[j] = ok ? sc[j] * a.scale_log2 : -INFINITY;
+          need |= sv[j] > m[c] + kRescaleLog2;
+        }
+        if (__any(need)) {
+          const float mx = max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+          const float mn = fmaxf(m[c], mx);
+          const float alpha = (m[c] == -INFINITY) ? 0.0f : fast_exp2(m[c] - mn);
+          l[c] *= alpha;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[c][mt] *= alpha;
+          m[c] = mn;
+        }
+        uint32_t ph[2], pl[2];
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+          const float p0 = sv[j] == -INFINITY ? 0.0f : fast_exp2(sv[j] - m[c]);
+          const float p1 = sv[j + 1] == -INFINITY ? 0.0f : fast_exp2(sv[j + 1] - m[c]);
+          l[c] += p0 + p1;
+          ph[j / 2] = Ops::pack2(p0, p1);
+          pl[j / 2] = Ops::pack2(p0 - Ops::lo(ph[j / 2]), p1 - Ops::hi(ph[j / 2]));
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint2 va = make_uint2(vt[mt][0], vt[mt][1]);
+          acc[c][mt] = Ops::pv(va, make_uint2(ph[0], ph[1]), acc[c][mt]);
+          acc[c][mt] = Ops::pv(va, make_uint2(pl[0], pl[1]), acc[c][mt]);
+        }
+      }
+    }
+    if (t + 1 < n_tiles) stash(stage ^ 1);
+    __syncthreads();
+  }
+
+  // ---- normalise and write each live row: lane (row i16, group grp) holds d = 16 mt + 4 grp + 0..3.
+  using S = typename Elem<DT>::S;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float lt = sum4(l[c]);
+    if (!live[c]) continue;
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    const int tok = tok_lo + (w * NC + c) * TPC + i16 / QR;
+    const int g = i16 % QR;
+    S* orow = reinterpret_cast<S*>(a.out) + (static_cast<int64_t>(q0) + tok) * a.out_st +
+              static_cast<int64_t>(kvh * G + g) * a.out_sh;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint32_t w0 = Ops::pack2(acc[c][mt][0] * inv, acc[c][mt][1] * inv);
+      const uint32_t w1 = Ops::pack2(acc[c][mt][2] * inv, acc[c][mt][3] * inv);
+      *reinterpret_cast<uint2*>(orow + 16 * mt + 4 * grp) = make_uint2(w0, w1);
+    }
+  }
+}
+
+constexpr int kNC = 2;  // column blocks per wavefront
+
+template <int DT, int D, int QR>
+int launch_shape(const PrefillArgs& a, int num_seqs, int max_q_len, hipStream_t s) {
+  constexpr int TQ = kPW * kNC * (16 / QR);
+  const int zb = (max_q_len + TQ - 1) / TQ;
+  hipLaunchKernelGGL((paged_prefill_kernel<DT, D, QR, kNC>), dim3(a.hkv, num_seqs, zb), dim3(kPW * kWave), 0, s, a);
+  return status_from_hip(hipGetLastError());
+}
+
+template <int DT>
+int launch_dt(const PrefillArgs& a, int d, int qr, int num_seqs, int max_q_len, hipStream_t s) {
+  if (d == 64) return qr == 8 ? launch_shape<DT, 64, 8>(a, num_seqs, max_q_len, s)
+                              : launch_shape<DT, 64, 16>(a, num_seqs, max_q_len, s);
+  return qr == 8 ? launch_shape<DT, 128, 8>(a, num_seqs, max_q_len, s)
+                 : launch_shape<DT, 128, 16>(a, num_seqs, max_q_len, s);
+}
+
+}  // namespace
+}  // namespace prefill
+}  // namespace mip
+
+using namespace mip;
+
+extern "C" int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_stride_head, const void* q,
+                                 int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                                 const void* v_cache, int64_t num_cache_blocks, const int32_t* block_tables,
+                                 int64_t bt_stride, const int32_t* cu_q, const int32_t* ctx_start,
+                                 int32_t num_seqs, int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq, float scale,
+                                 int32_t dtype, void* stream) {
+  if (dtype != MIP_F32 && dtype != MIP_F16 && dtype != MIP_BF16) return MIP_EINVAL;
+  if (num_seqs < 0 || max_q_len < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return MIP_EINVAL;
+  if (head_dim <= 0 || num_cache_blocks <= 0 || max_blocks_per_seq <= 0 || bt_stride < max_blocks_per_seq) return MIP_EINVAL;
+  if (!is_pow2(block_size) || block_size > 4096) return MIP_EINVAL;
+  if (num_seqs == 0 || max_q_len == 0) return MIP_OK;
+  if (!out || !q || !k_cache || !v_cache || !block_tables || !cu_q || !ctx_start) return MIP_EINVAL;
+  const int group = num_heads / num_kv_heads;
+  if (dtype == MIP_F32 || (head_dim != 64 && head_dim != 128) || group > 16) return MIP_EUNSUPPORTED;
+  if (num_seqs > 65535 || (max_q_len + 7) / 8 > 65535) return MIP_EUNSUPPORTED;
+  // q rows are read and output rows written 16 / 8 bytes at a time.
+  const uint64_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+                         static_cast<uint64_t>(q_stride_tok * 2) | static_cast<uint64_t>(q_stride_head * 2) |
+                         static_cast<uint64_t>(out_stride_tok * 2) | static_cast<uint64_t>(out_stride_head * 2);
+  if (align & 7) return MIP_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(q) | static_cast<uint64_t>(q_stride_tok * 2) |
+       static_cast<uint64_t>(q_stride_head * 2)) & 15)
+    return MIP_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return MIP_EINVAL;
+  if (num_cache_blocks > INT32_MAX) return MIP_EINVAL;
+
+  prefill::PrefillArgs a;
+  a.out = static_cast<char*>(out);
+  a.out_st = out_stride_tok;
+  a.out_sh = out_stride_head;
+  a.q = static_cast<const char*>(q);
+  a.q_st = q_stride_tok;
+  a.q_sh = q_stride_head;
+  a.k = static_cast<const char*>(k_cache);
+  a.v = static_cast<const char*>(v_cache);
+  a.ncb = num_cache_blocks;
+  a.bt = block_tables;
+  a.bt_stride = bt_stride;
+  a.cu_q = cu_q;
+  a.ctx_start = ctx_start;
+  a.hkv = num_kv_heads;
+  a.group = group;
+  a.bs = block_size;
+  a.log2_bs = ilog2_exact(block_size);
+  a.max_blocks = max_blocks_per_seq;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const int qr = group <= 8 ? 8 : 16;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == MIP_BF16) return prefill::launch_dt<MIP_BF16>(a, head_dim, qr, num_seqs, max_q_len, s);
+  return prefill::launch_dt<MIP_F16>(a, head_dim, qr, num_seqs, max_q_len, s);
+}

@@ -25,6 +25,7 @@ EXPORTED = (
     "mip_paged_decode_workspace",
     "mip_paged_decode_plan",
     "mip_paged_decode_plan_bytes",
+    "mip_paged_prefill",
     "mip_copy_blocks",
 )
 
@@ -59,6 +60,11 @@ _SIGNATURES = {
     "mip_paged_decode_plan": (
         _c.c_int,
         [_vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
+    "mip_paged_prefill": (
+        _c.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp],
     ),
     "mip_copy_blocks": (_c.c_int, [_vp, _vp, _vp, _i32, _i32, _i64, _i64, _vp]),
 }

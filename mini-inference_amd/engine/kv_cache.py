@@ -448,9 +448,11 @@ class PackedPrefillContext:
     """Several prompts packed end to end in one forward pass (engine/kv_cache.py:218-301).
 
     The scatter of the N packed tokens into the pool is the append kernel. Attention over
-    the packed tokens (block-diagonal causal mask, plus read-back of a cached prefix when
-    some sequence already has tokens) is torch SDPA, as in the reference. ``fuse_rope`` as
-    for :class:`PagedDecodeContext`.
+    the packed tokens (block-diagonal causal, plus any cached prefix of each sequence) is the
+    paged prefill kernel (``mip_paged_prefill``), which reads every key in place through the
+    block tables. Shapes it does not cover (fp32, head_dim other than 64/128) use torch SDPA
+    with the reference's mask and read-back, as the reference does. ``fuse_rope`` as for
+    :class:`PagedDecodeContext`.
     """
 
     fuse_rope = True
@@ -465,8 +467,6 @@ class PackedPrefillContext:
                 raise ValueError(f"no room in the KV cache for {start + n} tokens")
         cache.prepare_writes(self.slots, self.starts, self.lengths)
         dev = cache.k.device
-        seg = torch.repeat_interleave(torch.arange(len(self.slots), device=dev),
-                                      torch.tensor(self.lengths, device=dev))
         self.positions = torch.from_numpy(np.concatenate(
             [np.arange(a, a + n, dtype=np.int64) for a, n in zip(self.starts, self.lengths)])).to(dev)
         blocks, offsets = cache._write_index_np(self.slots, self.starts, self.lengths)
@@ -475,18 +475,55 @@ class PackedPrefillContext:
         self.write_at = (both[:n_tok], both[n_tok:2 * n_tok])
         self.slot_mapping = both[2 * n_tok:]
         self.has_prefix = any(self.starts)
+        self.ends = [a + n for a, n in zip(self.starts, self.lengths)]
+        # Inputs of the paged prefill kernel: packed row offsets, cached lengths, tables.
+        self.max_q_len = max(self.lengths) if self.lengths else 0
+        nb = max(1, cache.blocks_for(max(self.ends))) if self.ends else 1
+        tables = np.zeros((len(self.slots), nb), dtype=np.int32)
+        for i, s in enumerate(self.slots):
+            row = cache.block_tables[s][:nb]
+            tables[i, :len(row)] = row
+        cu = np.zeros(len(self.slots) + 1, dtype=np.int32)
+        cu[1:] = np.cumsum(self.lengths)
+        i32 = torch.from_numpy(np.concatenate([cu, np.asarray(self.starts, dtype=np.int32), tables.reshape(-1)])).to(dev)
+        s_n = len(self.slots)
+        self.cu_q, self.ctx_start = i32[:s_n + 1], i32[s_n + 1:2 * s_n + 1]
+        self.block_tables = i32[2 * s_n + 1:].view(s_n, nb)
+        self._mask_built = False
+        self._mask = None
+        self._read_at = None
+        self.last_index = torch.tensor(self.lengths, device=dev).cumsum(0) - 1
+
+    def _build_mask(self) -> None:
+        """The reference's mask and read-back index (engine/kv_cache.py:262-279), built on demand."""
+        cache, dev = self.cache, self.cache.k.device
+        seg = torch.repeat_interleave(torch.arange(len(self.slots), device=dev), torch.tensor(self.lengths, device=dev))
         if self.has_prefix:
-            ends = [a + n for a, n in zip(self.starts, self.lengths)]
-            self.read_at = cache.write_index(self.slots, [0] * len(self.slots), ends)
-            key_seg = torch.repeat_interleave(torch.arange(len(self.slots), device=dev), torch.tensor(ends, device=dev))
-            key_pos = torch.cat([torch.arange(e, device=dev) for e in ends])
-            self.mask = (seg[:, None] == key_seg[None, :]) & (key_pos[None, :] <= self.positions[:, None])
+            self._read_at = cache.write_index(self.slots, [0] * len(self.slots), self.ends)
+            key_seg = torch.repeat_interleave(torch.arange(len(self.slots), device=dev),
+                                              torch.tensor(self.ends, device=dev))
+            key_pos = torch.cat([torch.arange(e, device=dev) for e in self.ends])
+            self._mask = (seg[:, None] == key_seg[None, :]) & (key_pos[None, :] <= self.positions[:, None])
         elif len(self.slots) == 1:
-            self.mask = None
+            self._mask = None
         else:
             idx = torch.arange(seg.shape[0], device=dev)
-            self.mask = (seg[:, None] == seg[None, :]) & (idx[None, :] <= idx[:, None])
-        self.last_index = torch.tensor(self.lengths, device=dev).cumsum(0) - 1
+            self._mask = (seg[:, None] == seg[None, :]) & (idx[None, :] <= idx[:, None])
+        self._mask_built = True
+
+    @property
+    def mask(self) -> torch.Tensor | None:
+        """The reference's ``[N, keys]`` bool mask (None for one fresh prompt); built on demand."""
+        if not self._mask_built:
+            self._build_mask()
+        return self._mask
+
+    @property
+    def read_at(self) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """``(block, offset)`` of every sequence's keys ``0 .. end-1`` (prefix hits only)."""
+        if not self._mask_built:
+            self._build_mask()
+        return self._read_at
 
     def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
@@ -507,6 +544,12 @@ class PackedPrefillContext:
         return self._attention(k_layer, v_layer, q, k, v)
 
     def _attention(self, k_layer, v_layer, q, k, v) -> torch.Tensor:
+        c = self.cache
+        if paged_ops.prefill_supported(c.head_dim, q.shape[1], c.num_kv_heads, q.dtype):
+            # q is [1, Hq, N, D]; the kernel takes the [N, Hq, D] view and returns [N, Hq, D].
+            out = paged_ops.paged_prefill(q[0].transpose(0, 1), k_layer, v_layer, self.block_tables, self.cu_q,
+                                          self.ctx_start, self.max_q_len, scale=1.0 / (c.head_dim ** 0.5))
+            return out.transpose(0, 1).unsqueeze(0)
         if self.has_prefix:
             rb, ro = self.read_at
             keys = k_layer[rb, :, ro].transpose(0, 1).unsqueeze(0)

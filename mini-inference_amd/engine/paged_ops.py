@@ -319,6 +319,57 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     return out
 
 
+PREFILL_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def prefill_supported(head_dim: int, num_heads: int, num_kv_heads: int, dtype: torch.dtype) -> bool:
+    """Whether :func:`paged_prefill` has a kernel for this shape (16-bit, D 64/128, group <= 16)."""
+    return (dtype in PREFILL_DTYPES and head_dim in (64, 128) and num_heads % num_kv_heads == 0
+            and num_heads // num_kv_heads <= 16)
+
+
+def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                  cu_q: torch.Tensor, ctx_start: torch.Tensor, max_q_len: int, scale: float | None = None,
+                  out: torch.Tensor | None = None, max_blocks: int | None = None) -> torch.Tensor:
+    """Varlen causal attention of packed new tokens over their sequences' paged keys.
+
+    ``q``: ``[N, Hq, D]`` packed rows (last dim contiguous); sequence ``s`` owns rows
+    ``cu_q[s] .. cu_q[s+1]-1`` (int32 ``[S+1]``), at positions ``ctx_start[s] + i``
+    (int32 ``[S]``), and each row attends its sequence's keys ``0 .. position`` read from the
+    pool through ``block_tables`` (int32 ``[S, >= max_blocks]``). Returns ``out [N, Hq, D]``.
+    Follows engine/kv_cache.py:268-294 (prefix read-back + mask) and :290-294 (packed causal).
+    """
+    _require_device(q, k_cache, v_cache, block_tables, cu_q, ctx_start)
+    if q.dim() != 3 or q.stride(2) != 1:
+        raise ValueError("q must be [N, Hq, D] with a contiguous last dimension")
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache must be contiguous [num_blocks, Hkv, block_size, D] tensors of one shape")
+    nb1, hkv, bs, d = k_cache.shape
+    n, hq, dq = q.shape
+    if dq != d or hq % hkv:
+        raise ValueError(f"q {tuple(q.shape)} does not match the pool (Hkv={hkv}, D={d})")
+    if q.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
+        raise TypeError("q and the cache must share one dtype")
+    if block_tables.dtype != torch.int32 or cu_q.dtype != torch.int32 or ctx_start.dtype != torch.int32:
+        raise TypeError("block_tables, cu_q and ctx_start must be int32")
+    num_seqs = ctx_start.shape[0]
+    if block_tables.dim() != 2 or block_tables.shape[0] < num_seqs or block_tables.stride(1) != 1:
+        raise ValueError("block_tables must be [S, nb] with contiguous rows")
+    if cu_q.shape != (num_seqs + 1,) or not (cu_q.is_contiguous() and ctx_start.is_contiguous()):
+        raise ValueError("cu_q must be int32 [S + 1] and ctx_start int32 [S], contiguous")
+    nbm = block_tables.shape[1] if max_blocks is None else max_blocks
+    if out is None:
+        out = torch.empty(n, hq, d, dtype=q.dtype, device=q.device)
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    lib = _native.load()
+    st = lib.mip_paged_prefill(out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1),
+                               k_cache.data_ptr(), v_cache.data_ptr(), nb1, block_tables.data_ptr(),
+                               block_tables.stride(0), cu_q.data_ptr(), ctx_start.data_ptr(), num_seqs, max_q_len, hq,
+                               hkv, d, bs, nbm, scale, dtype_code(q.dtype), _stream_ptr(q.device))
+    _native.check(st, "mip_paged_prefill")
+    return out
+
+
 def paged_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
                         v_cache: torch.Tensor, slot_mapping: torch.Tensor, block_tables: torch.Tensor,
                         context_lens: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,

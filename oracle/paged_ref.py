@@ -16,7 +16,10 @@ Each function restates one piece of the reference (Ham12-3/mini-inference) and c
   decode_attention     engine/model.py:126-147      GQA regroup + SDPA with a [B,1,1,kv_len] bool mask
   sdpa_attention       engine/model.py:101-123      GQA by repeat_interleave + SDPA
   paged_decode_torch   engine/kv_cache.py:611-620   append + gather + decode_attention (the reference path)
+  packed_prefill_torch engine/kv_cache.py:262-294   prefix read-back + dense [N, keys] mask + SDPA
   attention_f64        (independent)                float64 brute force over each sequence's own keys
+  prefill_attention_f64  engine/kv_cache.py:268-294  float64 packed prefill: each new token over its own
+                                                    sequence's keys 0..position (prefix + new tokens)
   copy_blocks          (no reference counterpart)   bitwise k[:, dst] = k[:, src] for every layer
 
 Arrays: the pool of one layer is ``[num_blocks + 1, Hkv, block_size, D]`` (reference layout,
@@ -240,6 +243,29 @@ def paged_decode_torch(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Te
     return decode_attention(q, keys, values, attn_mask=mask)
 
 
+def packed_prefill_torch(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                         tables: Sequence[Sequence[int]], starts: Sequence[int], lengths: Sequence[int],
+                         block_size: int) -> torch.Tensor:
+    """The reference's packed prefill attention with cached prefixes (engine/kv_cache.py:262-294).
+
+    Every sequence's keys ``0 .. end-1`` are read back from the pool (``write_index``), and
+    SDPA runs over all of them with the dense mask ``key_seg == seg & key_pos <= position``.
+    ``q`` ``[1, Hq, N, D]`` (float32), pools ``[NB, Hkv, bs, D]``; returns ``[1, Hq, N, D]``.
+    """
+    nseq = len(lengths)
+    ends = [a + n for a, n in zip(starts, lengths)]
+    seg = torch.repeat_interleave(torch.arange(nseq), torch.tensor(list(lengths)))
+    positions = torch.cat([torch.arange(a, a + n) for a, n in zip(starts, lengths)])
+    rb, ro = write_index(tables, range(nseq), [0] * nseq, ends, block_size)
+    rb, ro = torch.from_numpy(rb), torch.from_numpy(ro)
+    keys = k_layer[rb, :, ro].transpose(0, 1).unsqueeze(0)     # [1, Hkv, total keys, D]
+    values = v_layer[rb, :, ro].transpose(0, 1).unsqueeze(0)
+    key_seg = torch.repeat_interleave(torch.arange(nseq), torch.tensor(ends))
+    key_pos = torch.cat([torch.arange(e) for e in ends])
+    mask = (seg.unsqueeze(1) == key_seg.unsqueeze(0)) & (key_pos.unsqueeze(0) <= positions.unsqueeze(1))
+    return sdpa_attention(q, keys, values, attn_mask=mask)
+
+
 # --------------------------------------------------------------------------- attention (float64 brute force)
 
 
@@ -272,4 +298,43 @@ def attention_f64(q: np.ndarray, k_layer: np.ndarray, v_layer: np.ndarray, table
             s -= s.max(axis=1, keepdims=True)
             w = np.exp(s)
             out[b, heads] = (w @ vals) / w.sum(axis=1, keepdims=True)
+    return out
+
+
+def prefill_attention_f64(q: np.ndarray, k_layer: np.ndarray, v_layer: np.ndarray, tables: Sequence[Sequence[int]],
+                          starts: Sequence[int], lengths: Sequence[int], block_size: int,
+                          scale: float | None = None) -> np.ndarray:
+    """Independent float64 packed prefill over paged keys (engine/kv_cache.py:268-294).
+
+    ``q`` ``[N, Hq, D]`` packed rows, sequence s owning ``lengths[s]`` consecutive rows; its
+    new token i sits at position ``starts[s] + i`` and attends keys ``0 .. starts[s] + i`` of
+    its own sequence (prefix and earlier new tokens), read from the pool through ``tables[s]``
+    (pools ``[NB, Hkv, bs, D]`` float values, already holding the new keys). Query head h reads
+    kv head h // (Hq // Hkv). Returns ``[N, Hq, D]`` float64.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    n_all, hq, d = q.shape
+    hkv = k_layer.shape[1]
+    group = hq // hkv
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    out = np.zeros((n_all, hq, d), dtype=np.float64)
+    row = 0
+    for s, (start, n) in enumerate(zip(starts, lengths)):
+        end = start + n
+        j = np.arange(end)
+        blk = np.asarray(tables[s], dtype=np.int64)[j // block_size]
+        off = j % block_size
+        pos = start + np.arange(n)
+        allowed = j[None, :] <= pos[:, None]                                  # [n, end] causal over positions
+        for kv in range(hkv):
+            keys = np.asarray(k_layer[blk, kv, off], dtype=np.float64)        # [end, D]
+            vals = np.asarray(v_layer[blk, kv, off], dtype=np.float64)
+            for g in range(group):
+                h = kv * group + g
+                sc = q[row:row + n, h] @ keys.T * scale                       # [n, end]
+                sc = np.where(allowed, sc, -np.inf)
+                sc -= sc.max(axis=1, keepdims=True)
+                w = np.exp(sc)
+                out[row:row + n, h] = (w @ vals) / w.sum(axis=1, keepdims=True)
+        row += n
     return out

@@ -1,0 +1,199 @@
+"""GPU parity of the paged prefill attention kernel (``mip_paged_prefill``) through the C ABI.
+
+Bar: within 2e-3 beyond the output's own final rounding (half an ulp) of the float64 oracle
+(oracle/paged_ref.py ``prefill_attention_f64``) on the same 16-bit inputs, as for decode.
+The cache context's kernel path also matches the reference's own path (prefix read-back +
+dense mask + SDPA, engine/kv_cache.py:262-294).
+"""
+
+from __future__ import annotations
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import paged_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16}
+MANTISSA_BITS = {"float16": 10, "bfloat16": 7}
+
+
+def half_ulp(x: np.ndarray, dtype: str) -> np.ndarray:
+    ax = np.maximum(np.abs(x), np.finfo(np.float32).tiny)
+    return 0.5 * np.exp2(np.floor(np.log2(ax)) - MANTISSA_BITS[dtype])
+
+
+def build(gpu, dtype, d, hq, hkv, bs, starts, lengths, seed=0, stale_nan=False, extra_blocks=3):
+    """Scattered pool holding every sequence's keys 0..end-1; padded int32 tables; packed q."""
+    rnd = random.Random(seed)
+    ends = [a + n for a, n in zip(starts, lengths)]
+    need = [(e + bs - 1) // bs for e in ends]
+    nb = sum(need) + extra_blocks
+    ids = list(range(nb))
+    rnd.shuffle(ids)
+    tables, cur = [], 0
+    for k in need:
+        tables.append(ids[cur:cur + k])
+        cur += k
+    dt = DTYPES[dtype]
+    g = torch.Generator().manual_seed(seed)
+    k_pool = torch.randn(nb + 1, hkv, bs, d, generator=g).to(dt)
+    v_pool = torch.randn(nb + 1, hkv, bs, d, generator=g).to(dt)
+    if stale_nan:  # rows past each sequence's last key must never be read
+        for t, e in zip(tables, ends):
+            last, used = t[-1], e - (len(t) - 1) * bs
+            k_pool[last, :, used:] = float("nan")
+            v_pool[last, :, used:] = float("nan")
+    # q as the packed [N, Hq, D] view of a wider qkv row, like the model's projection output.
+    n_all = sum(lengths)
+    qkv = torch.randn(n_all, (hq + 2 * hkv) * d, generator=g).to(dt)
+    q = qkv[:, :hq * d].view(n_all, hq, d)
+    width = max(need) + 1
+    tab = torch.full((len(lengths), width), 0, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        tab[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    cu = torch.zeros(len(lengths) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lengths), 0)
+    dev = dict(q=qkv.to(gpu)[:, :hq * d].view(n_all, hq, d), k=k_pool.to(gpu), v=v_pool.to(gpu), tab=tab.to(gpu),
+               cu=cu.to(gpu), st=torch.tensor(starts, dtype=torch.int32).to(gpu))
+    want = ref.prefill_attention_f64(q.float().numpy(), k_pool.float().numpy(), v_pool.float().numpy(), tables,
+                                     starts, lengths, bs)
+    return dev, want
+
+
+CASES = [
+    ([0, 0, 0], [1, 17, 40]),             # fresh prompts, block-diagonal causal
+    ([37, 0, 512, 3], [5, 33, 100, 1]),   # cached prefixes at unaligned positions
+    ([16], [64]),                         # one sequence, block-aligned prefix
+]
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("d,hq,hkv,bs", [(64, 14, 2, 16), (128, 28, 4, 32), (64, 8, 8, 16), (64, 16, 1, 16),
+                                         (128, 7, 1, 4)])
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_paged_prefill_matches_f64(gpu, dtype, d, hq, hkv, bs, case):
+    from engine import paged_ops
+
+    starts, lengths = CASES[case]
+    announce(f"paged_prefill {dtype} d={d} hq={hq} hkv={hkv} bs={bs} starts={starts} lengths={lengths}")
+    dev, want = build(gpu, dtype, d, hq, hkv, bs, starts, lengths, seed=case)
+    out = paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], max(lengths))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    err = float((np.abs(got - want) - half_ulp(want, dtype)).max())
+    assert err <= 2e-3, err
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+def test_paged_prefill_never_reads_stale_rows(gpu, dtype):
+    from engine import paged_ops
+
+    announce(f"paged_prefill stale NaN rows {dtype}")
+    starts, lengths = [21, 0, 7], [11, 29, 2]
+    dev, want = build(gpu, dtype, 64, 14, 2, 16, starts, lengths, seed=7, stale_nan=True)
+    out = paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], max(lengths))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert float((np.abs(got - want) - half_ulp(want, dtype)).max()) <= 2e-3
+
+
+def test_paged_prefill_max_q_len_larger_than_needed_and_empty_sequences(gpu):
+    """Extra grid blocks (a loose max_q_len) and sequences with no new tokens write nothing."""
+    from engine import paged_ops
+
+    announce("paged_prefill loose max_q_len, empty sequences")
+    starts, lengths = [4, 9, 0], [6, 0, 3]
+    dev, want = build(gpu, "bfloat16", 64, 14, 2, 16, starts, lengths, seed=9)
+    out = torch.full((sum(lengths), 14, 64), 7.0, dtype=torch.bfloat16, device=gpu)
+    paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], 200, out=out)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert float((np.abs(got - want) - half_ulp(want, "bfloat16")).max()) <= 2e-3
+
+
+def test_paged_prefill_config4_prefix_hits(gpu):
+    """Config 4's prefill: 64 requests on a 512-token cached prefix + suffix U[32, 512], fp16,
+    Qwen2.5-0.5B attention shape; rows of 8 sampled sequences checked against float64."""
+    from engine import paged_ops
+
+    announce("paged_prefill config 4 (64 x (512 prefix + U[32,512]) fp16)")
+    rnd = random.Random(4)
+    lengths = [rnd.randint(32, 512) for _ in range(64)]
+    starts = [512] * 64
+    dtype, d, hq, hkv, bs = "float16", 64, 14, 2, 16
+    # Full-size inputs (the oracle runs on a sample of sequences).
+    ends = [a + n for a, n in zip(starts, lengths)]
+    need = [(e + bs - 1) // bs for e in ends]
+    nb = sum(need) + 8
+    ids = list(range(nb))
+    rnd.shuffle(ids)
+    tables, cur = [], 0
+    for k in need:
+        tables.append(ids[cur:cur + k])
+        cur += k
+    g = torch.Generator(device=gpu).manual_seed(11)
+    k_pool = torch.randn(nb + 1, hkv, bs, d, generator=g, device=gpu).half()
+    v_pool = torch.randn(nb + 1, hkv, bs, d, generator=g, device=gpu).half()
+    n_all = sum(lengths)
+    qkv = torch.randn(n_all, (hq + 2 * hkv) * d, generator=g, device=gpu).half()
+    q = qkv[:, :hq * d].view(n_all, hq, d)
+    tab = torch.zeros(64, max(need), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        tab[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    cu = torch.zeros(65, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lengths), 0)
+    out = paged_ops.paged_prefill(q, k_pool, v_pool, tab.to(gpu), cu.to(gpu), torch.tensor(starts, dtype=torch.int32,
+                                  device=gpu), max(lengths))
+    torch.cuda.synchronize()
+    kp, vp = k_pool.float().cpu().numpy(), v_pool.float().cpu().numpy()
+    qc, oc = q.float().cpu().numpy(), out.float().cpu().numpy()
+    for s in (0, 5, 17, 30, 41, 50, 58, 63):
+        r0, r1 = int(cu[s]), int(cu[s + 1])
+        want = ref.prefill_attention_f64(qc[r0:r1], kp, vp, [tables[s]], [starts[s]], [lengths[s]], bs)
+        err = float((np.abs(oc[r0:r1] - want) - half_ulp(want, dtype)).max())
+        assert err <= 2e-3, (s, err)
+
+
+@pytest.mark.parametrize("prefix", [False, True])
+@torch.inference_mode()
+def test_prefill_context_kernel_matches_reference_path(gpu, prefix, monkeypatch):
+    """PackedPrefillContext: the kernel path against the reference's read-back + mask SDPA path."""
+    from engine import paged_ops
+    from engine.kv_cache import PagedKVCache
+
+    announce(f"prefill context kernel vs reference SDPA path, prefix={prefix}")
+    dt, d, hq, hkv, bs = torch.bfloat16, 64, 14, 2, 16
+    starts = [40, 0, 17] if prefix else [0, 0, 0]
+    new = [23, 50, 9]
+    outs = []
+    for use_kernel in (True, False):
+        cache = PagedKVCache(1, hkv, d, num_blocks=64, block_size=bs, max_seqs=4, max_len=256, dtype=dt, device=gpu)
+        slots = []
+        for st, n in zip(starts, new):
+            s = cache.allocate(st + n)
+            cache.lengths[s] = st
+            slots.append(s)
+        gen = torch.Generator(device=gpu).manual_seed(5)
+        cache.k.normal_(0.0, 1.0, generator=gen)
+        cache.v.normal_(0.0, 1.0, generator=gen)
+        ctx = cache.packed_prefill_context(slots, new)
+        n = sum(new)
+        qkv = torch.randn(1, n, (hq + 2 * hkv) * d, generator=gen, device=gpu).to(dt)
+        q, k, v = qkv.split([hq * d, hkv * d, hkv * d], dim=-1)
+        q = q.view(1, n, hq, d).transpose(1, 2)
+        k = k.view(1, n, hkv, d).transpose(1, 2)
+        v = v.view(1, n, hkv, d).transpose(1, 2)
+        if not use_kernel:
+            monkeypatch.setattr(paged_ops, "prefill_supported", lambda *a: False)
+        outs.append(ctx.attend(0, q, k, v).float())
+        monkeypatch.undo()
+    torch.cuda.synchronize()
+    err = (outs[0] - outs[1]).abs().max().item()
+    assert err <= 1.6e-2, err  # both sides round to bf16; the reference path also rounds P and its sums

@@ -293,6 +293,16 @@ def test_abi_host_checks_return_before_launch(lib):
     assert rope(*dt) == E                               # unknown dtype
     bs = list(rargs); bs[20] = 24
     assert rope(*bs) == E                               # block size not a power of two
+    pf = lib.mip_paged_prefill
+    pargs = [None, 896, 64, None, 1152, 64, None, None, 64, None, 8, None, None, 0, 16, 14, 2, 64, 16, 8, 0.125,
+             _native.MIP_BF16, None]
+    assert pf(*pargs) == OK                             # no sequences
+    g = list(pargs); g[13], g[16] = 2, 3
+    assert pf(*g) == E                                  # 14 heads do not split over 3 kv heads
+    st = list(pargs); st[13], st[10] = 2, 4
+    assert pf(*st) == E                                 # table stride below max_blocks
+    nul = list(pargs); nul[13] = 2
+    assert pf(*nul) == E                                # null pointers
     cp = lib.mip_copy_blocks
     assert cp(None, None, None, 0, 24, 100, 8192, None) == OK
     assert cp(None, None, None, 3, 0, 100, 8192, None) == E
