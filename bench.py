@@ -20,6 +20,8 @@ Reported (one JSON line on stdout):
                 with GEMMs, RoPE + append (one fused kernel, mip_rope_kv_append), attention,
                 MLP, final norm, logits), the step replayed as one captured HIP graph
                 (engine/cuda_graphs.py); decode_tok_s_eager: the same step launched eagerly
+  prefill       packed prefill attention over a cached prefix (64 forks of a 520-token prefix,
+                suffixes U[32, 512], fp16): time per layer and TFLOP/s against the fp16 MFMA peak
   cpu_baseline  the reference's torch CPU path (index_put_ append + table gather + SDPA,
                 the oracle's restatement) timed on this host's cores for one layer, fp32
 
@@ -177,6 +179,51 @@ def decode_tok_s(batch, steps: int, warmup: int) -> dict:
             "eager_ms_per_step": t_eager * 1e3, "steps": steps}
 
 
+def prefill_measure(dev, iters: int = 30) -> dict:
+    """Packed prefill attention of the shared-prefix workload (64 forks of a 520-token cached
+    prefix, suffixes U[32, 512], fp16, 14q/2kv heads d64, block 16), one layer, HIP events.
+
+    The new tokens attend their sequence's cached prefix and their own earlier tokens through
+    the paged prefill kernel (``mip_paged_prefill``); flops = 4 * D * Hq * sum(position + 1).
+    """
+    import torch
+
+    from engine import paged_ops, workloads
+
+    pb = workloads.build_prefix_batch(dev, seed=0, num_layers=1)
+    ctx = pb.cache.packed_prefill_context(pb.children, pb.suffix_lens)  # appends nothing; CoW of the shared block
+    hq, d = 14, 64
+    n = sum(pb.suffix_lens)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(n, hq, d, generator=gen, device=dev).half()
+    out = torch.empty_like(q)
+    k_layer, v_layer = pb.cache.k[0], pb.cache.v[0]
+
+    def call():
+        paged_ops.paged_prefill(q, k_layer, v_layer, ctx.block_tables, ctx.cu_q, ctx.ctx_start, ctx.max_q_len,
+                                out=out)
+
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    t = time_loop(call, iters)
+    keys = sum(sum(a + i + 1 for i in range(m)) for a, m in zip(ctx.starts, pb.suffix_lens))
+    tflops = 4 * d * hq * keys / t / 1e12
+    return {
+        "workload": f"packed prefill attention over a cached prefix: {len(pb.children)} forks of a "
+                    f"{pb.prefix_len}-token prefix + suffixes U[32,512] ({n} new tokens), fp16, 14q/2kv heads d64, "
+                    "block 16, one layer",
+        "kernel": "paged_prefill_kernel<f16, D=64, QR=8, NC=4>",
+        "us_per_layer": round(t * 1e6, 1),
+        "bound": "mfma",
+        "achieved": round(tflops, 1),
+        "peak": 2500.0,
+        "unit": "TFLOP/s",
+        "frac": round(tflops / 2500.0, 4),
+        "keys_attended": keys,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -185,6 +232,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (about)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-model", action="store_true", help="skip the full-model decode tok/s measurement")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the packed prefill attention measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 512 MiB device copy three times (HBM counter scale for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -310,6 +358,15 @@ def main() -> int:
         except Exception as exc:  # the headline kernel numbers stand on their own
             log(f"full-model decode failed: {exc!r}")
             result["decode_tok_s"] = None
+
+    if not args.no_prefill:
+        try:
+            result["prefill"] = prefill_measure(dev)
+            pf = result["prefill"]
+            log(f"prefill attention: {pf['us_per_layer']} us/layer, {pf['achieved']} TFLOP/s ({pf['frac']:.1%} of peak)")
+        except Exception as exc:
+            log(f"prefill measurement failed: {exc!r}")
+            result["prefill"] = None
 
     if not args.no_cpu_baseline:
         cb = cpu_baseline(batch, qs[0], ks[0], vs[0], args.cpu_budget)

@@ -17,11 +17,12 @@
 //
 // Per 32-key tile: all 256 threads copy the K and V rows (found through the block table) into
 // an LDS stage (two stages: the next tile's rows are fetched into registers while the current
-// one is computed); then each wavefront, for each 16-key half:
+// one is computed); then each wavefront computes, for each 16-key half,
 //   S^T[16 keys x 16 rows] = K . Q^T      v_mfma_f32_16x16x32, D/32 steps (Q^T in registers)
-//   O^T[D x 16 rows]      += V^T . P^T    v_mfma_f32_16x16x16, D/16 tiles, P split hi + lo
+// and then, over all 32 keys,
+//   O^T[D x 16 rows]      += V^T . P^T    v_mfma_f32_16x16x32, D/16 tiles (bf16: P split hi + lo)
 // with a base-2 online softmax per row, as in the decode kernels. Rows whose position is below
-// a key mask it out; a wavefront skips halves that lie beyond all of its rows' positions.
+// a key mask it out; a wavefront skips tiles that lie beyond all of its rows' positions.
 #include "paged_decode_common.h"
 
 namespace mip {
@@ -33,8 +34,17 @@ using decode::fast_exp2;
 using decode::kRescaleLog2;
 using decode::MfmaOps;
 
-constexpr int kPW = 4;    // wavefronts per workgroup
-constexpr int kKT = 32;   // keys per LDS tile
+#ifndef MIP_PREFILL_KT
+#define MIP_PREFILL_KT 32
+#endif
+// Column blocks per wavefront: 4 at head_dim 64 (fewer barriers and K/V reads per row; 2
+// wavefronts per SIMD), 2 at head_dim 128 (register file).
+#ifndef MIP_PREFILL_NC
+#define MIP_PREFILL_NC 0
+#endif
+constexpr int kPW = 4;                 // wavefronts per workgroup
+constexpr int kKT = MIP_PREFILL_KT;    // keys per LDS tile (a multiple of 32)
+static_assert(kKT % 32 == 0, "tiles are whole 32-key PV steps");
 
 struct PrefillArgs {
   char* out;
@@ -64,6 +74,11 @@ __device__ __forceinline__ float max4(float x) {
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
+
+// P = exp2(s - m) lies in [0, 2^kRescaleLog2]. fp16 holds it to 2^-11 relative, enough for
+// the 2e-3 bound on outputs that are convex combinations of the values; bf16 (2^-8) is split
+// into a rounded part and its remainder, each multiplied by V^T.
+template <int DT> constexpr bool kSplitP = DT == MIP_BF16;
 
 template <int D>
 struct PShape {
@@ -130,9 +145,20 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
   }
   wave_pmax = __builtin_amdgcn_readfirstlane(wave_pmax < cap - 1 ? wave_pmax : cap - 1);
 
-  // ---- loader: this thread's K / V chunks of a tile.
+  // ---- loader: this thread's K / V chunks of a tile. The block ids of a tile are read one
+  // tile ahead of its rows, so the table lookup does not add a second latency per tile.
   uint4 kbuf[P::NLD], vbuf[P::NLD];
   bool okbuf[P::NLD];
+  int bid[P::NLD];
+  auto lookup = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < P::NLD; ++j) {
+      const int r = (tid + j * kPW * kWave) / CPR;
+      const int key = t * kKT + r;
+      const int kk = key < p_last ? key : p_last;
+      bid[j] = table[kk >> a.log2_bs];
+    }
+  };
   auto fetch = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < P::NLD; ++j) {
@@ -140,7 +166,7 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
       const int r = idx / CPR, c = idx % CPR;
       const int key = t * kKT + r;
       const int kk = key < p_last ? key : p_last;
-      const int b = table[kk >> a.log2_bs];
+      const int b = bid[j];
       const bool bok = b >= 0 && b < a.ncb;
       const bool ok = key <= p_last && bok;
       // Keys past the last position re-read that position's row (a real key, so finite V: the
@@ -173,73 +199,107 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
     for (int mt = 0; mt < MT; ++mt) acc[c][mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
+  lookup(0);
   fetch(0);
+  if (n_tiles > 1) lookup(1);
   stash(0);
   __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
     const int stage = t & 1;
-    if (t + 1 < n_tiles) fetch(t + 1);
-    const char* st = smem + stage * P::STAGE;
+    if (t + 1 < n_tiles) {
+      fetch(t + 1);
+      if (t + 2 < n_tiles) lookup(t + 2);
+    }
+    const char* st_tile = smem + stage * P::STAGE;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int key0 = t * kKT + 16 * u;
-      if (key0 > wave_pmax) break;  // every row of this wavefront sits before these keys
-      uint4 kreg[KC];
+    for (int h = 0; h < kKT / 32; ++h) {
+    const char* st = st_tile + h * 32 * RB;  // K rows of this 32-key step (V rows at + TILE)
+    const int key0 = t * kKT + 32 * h;
+    if (key0 <= wave_pmax) {  // else every row of this wavefront sits before these keys
+      // K operands of the two 16-key halves (keys 16u + i16).
+      uint4 kreg[2][KC];
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-        const int r = 16 * u + i16, ch = 4 * kc + grp;
-        kreg[kc] = *reinterpret_cast<const uint4*>(st + r * RB + ((ch ^ (r & (CPR - 1))) * 16));
+      for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          const int r = 16 * u + i16, ch = 4 * kc + grp;
+          kreg[u][kc] = *reinterpret_cast<const uint4*>(st + r * RB + ((ch ^ (r & (CPR - 1))) * 16));
+        }
       }
-      uint32_t vt[MT][2];
-      const uint16_t* vcol = reinterpret_cast<const uint16_t*>(st + P::TILE + (16 * u + 4 * grp) * RB) + i16;
+      // The PV product runs over all 32 keys at once (16x16x32). Its k index 8 grp + i stands
+      // for key 4 grp + i (i < 4) or 16 + 4 grp + i - 4: exactly the keys this lane's two S^T
+      // halves hold, so P needs no lane exchange; V^T is read in the same key order.
+      uint4 vt[MT];
+      const uint16_t* v0 = reinterpret_cast<const uint16_t*>(st + P::TILE + (4 * grp) * RB) + i16;
+      const uint16_t* v1 = v0 + 16 * D;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const uint32_t e0 = vcol[0 * D + 16 * mt], e1 = vcol[1 * D + 16 * mt];
-        const uint32_t e2 = vcol[2 * D + 16 * mt], e3 = vcol[3 * D + 16 * mt];
-        vt[mt][0] = e0 | (e1 << 16);
-        vt[mt][1] = e2 | (e3 << 16);
+        const int o = 16 * mt;
+        vt[mt].x = static_cast<uint32_t>(v0[o]) | (static_cast<uint32_t>(v0[D + o]) << 16);
+        vt[mt].y = static_cast<uint32_t>(v0[2 * D + o]) | (static_cast<uint32_t>(v0[3 * D + o]) << 16);
+        vt[mt].z = static_cast<uint32_t>(v1[o]) | (static_cast<uint32_t>(v1[D + o]) << 16);
+        vt[mt].w = static_cast<uint32_t>(v1[2 * D + o]) | (static_cast<uint32_t>(v1[3 * D + o]) << 16);
       }
-      bool kok[4];
+      bool kok[8];
+      int kidx[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) kok[j] = s_ok[stage][16 * u + 4 * grp + j] != 0;
+      for (int i = 0; i < 8; ++i) {
+        const int r = (i < 4 ? 0 : 12) + 4 * grp + i;
+        kok[i] = s_ok[stage][32 * h + r] != 0;
+        kidx[i] = key0 + r;
+      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        f32x4_t sc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4_t s0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc) sc = Ops::qk(kreg[kc], qreg[c][kc], sc);
-        float sv[4];
+        for (int kc = 0; kc < KC; ++kc) {
+          s0 = Ops::qk(kreg[0][kc], qreg[c][kc], s0);
+          s1 = Ops::qk(kreg[1][kc], qreg[c][kc], s1);
+        }
+        float sv[8];
         bool need = false;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bool ok = kok[j] && key0 + 4 * grp + j <= pos[c];
-          sv[j] = ok ? sc[j] * a.scale_log2 : -INFINITY;
-          need |= sv[j] > m[c] + kRescaleLog2;
+        for (int i = 0; i < 8; ++i) {
+          const float raw = i < 4 ? s0[i] : s1[i - 4];
+          sv[i] = (kok[i] && kidx[i] <= pos[c]) ? raw * a.scale_log2 : -INFINITY;
+          need |= sv[i] > m[c] + kRescaleLog2;
         }
         if (__any(need)) {
-          const float mx = max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
-          const float mn = fmaxf(m[c], mx);
+          float mx = sv[0];
+#pragma unroll
+          for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+          const float mn = fmaxf(m[c], max4(mx));
           const float alpha = (m[c] == -INFINITY) ? 0.0f : fast_exp2(m[c] - mn);
           l[c] *= alpha;
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) acc[c][mt] *= alpha;
           m[c] = mn;
         }
-        uint32_t ph[2], pl[2];
+        float pr[8];
 #pragma unroll
-        for (int j = 0; j < 4; j += 2) {
-          const float p0 = sv[j] == -INFINITY ? 0.0f : fast_exp2(sv[j] - m[c]);
-          const float p1 = sv[j + 1] == -INFINITY ? 0.0f : fast_exp2(sv[j + 1] - m[c]);
-          l[c] += p0 + p1;
-          ph[j / 2] = Ops::pack2(p0, p1);
-          pl[j / 2] = Ops::pack2(p0 - Ops::lo(ph[j / 2]), p1 - Ops::hi(ph[j / 2]));
+        for (int i = 0; i < 8; ++i) {
+          pr[i] = sv[i] == -INFINITY ? 0.0f : fast_exp2(sv[i] - m[c]);
+          l[c] += pr[i];
         }
+        uint4 ph;
+        ph.x = Ops::pack2(pr[0], pr[1]);
+        ph.y = Ops::pack2(pr[2], pr[3]);
+        ph.z = Ops::pack2(pr[4], pr[5]);
+        ph.w = Ops::pack2(pr[6], pr[7]);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const uint2 va = make_uint2(vt[mt][0], vt[mt][1]);
-          acc[c][mt] = Ops::pv(va, make_uint2(ph[0], ph[1]), acc[c][mt]);
-          acc[c][mt] = Ops::pv(va, make_uint2(pl[0], pl[1]), acc[c][mt]);
+        for (int mt = 0; mt < MT; ++mt) acc[c][mt] = Ops::qk(vt[mt], ph, acc[c][mt]);
+        if constexpr (kSplitP<DT>) {
+          // bf16 keeps only 8 bits of p: add the rounding remainder as a second product.
+          uint4 pl;
+          pl.x = Ops::pack2(pr[0] - Ops::lo(ph.x), pr[1] - Ops::hi(ph.x));
+          pl.y = Ops::pack2(pr[2] - Ops::lo(ph.y), pr[3] - Ops::hi(ph.y));
+          pl.z = Ops::pack2(pr[4] - Ops::lo(ph.z), pr[5] - Ops::hi(ph.z));
+          pl.w = Ops::pack2(pr[6] - Ops::lo(ph.w), pr[7] - Ops::hi(ph.w));
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[c][mt] = Ops::qk(vt[mt], pl, acc[c][mt]);
         }
       }
+    }
     }
     if (t + 1 < n_tiles) stash(stage ^ 1);
     __syncthreads();
@@ -265,13 +325,14 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
   }
 }
 
-constexpr int kNC = 2;  // column blocks per wavefront
+template <int D> constexpr int kNC = MIP_PREFILL_NC > 0 ? MIP_PREFILL_NC : (D == 64 ? 4 : 2);
 
 template <int DT, int D, int QR>
 int launch_shape(const PrefillArgs& a, int num_seqs, int max_q_len, hipStream_t s) {
-  constexpr int TQ = kPW * kNC * (16 / QR);
+  constexpr int NC = kNC<D>;
+  constexpr int TQ = kPW * NC * (16 / QR);
   const int zb = (max_q_len + TQ - 1) / TQ;
-  hipLaunchKernelGGL((paged_prefill_kernel<DT, D, QR, kNC>), dim3(a.hkv, num_seqs, zb), dim3(kPW * kWave), 0, s, a);
+  hipLaunchKernelGGL((paged_prefill_kernel<DT, D, QR, NC>), dim3(a.hkv, num_seqs, zb), dim3(kPW * kWave), 0, s, a);
   return status_from_hip(hipGetLastError());
 }
 
@@ -304,7 +365,7 @@ extern "C" int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_
   if (!out || !q || !k_cache || !v_cache || !block_tables || !cu_q || !ctx_start) return MIP_EINVAL;
   const int group = num_heads / num_kv_heads;
   if (dtype == MIP_F32 || (head_dim != 64 && head_dim != 128) || group > 16) return MIP_EUNSUPPORTED;
-  if (num_seqs > 65535 || (max_q_len + 7) / 8 > 65535) return MIP_EUNSUPPORTED;
+  if (num_seqs > 65535 || (max_q_len + 3) / 4 > 65535) return MIP_EUNSUPPORTED;
   // q rows are read and output rows written 16 / 8 bytes at a time.
   const uint64_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
                          static_cast<uint64_t>(q_stride_tok * 2) | static_cast<uint64_t>(q_stride_head * 2) |
