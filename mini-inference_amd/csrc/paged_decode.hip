@@ -900,8 +900,14 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
     sa.ws_prefix = reinterpret_cast<int*>(static_cast<char*>(workspace) + wl.prefix_off);
     sa.ws_rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.rec_off);
     sa.app = app;
-    sa.plan = static_cast<const int32_t*>(plan);
-    if (reinterpret_cast<uintptr_t>(plan) & 3) return MIP_EINVAL;
+    // A plan drives the tile-descriptor kernel, which needs tiles inside one block and 32-bit
+    // lane offsets into the q head rows; otherwise the kernel derives its split itself.
+    const bool use_plan = plan != nullptr && stream_plan_bytes(wl.stream, batch, num_kv_heads, block_size,
+                                                               max_blocks_per_seq) > 0 &&
+                          q_stride_h >= 0 && q_stride_h * 2 * 16 < (int64_t{1} << 31);
+    if (plan && (reinterpret_cast<uintptr_t>(plan) & 7)) return MIP_EINVAL;
+    sa.plan = use_plan ? static_cast<const int32_t*>(plan) : nullptr;
+    sa.nrows = static_cast<uint32_t>(num_cache_blocks * num_kv_heads * block_size);
     const int64_t lim = int64_t{1} << 31;
     for (const int64_t x : {q_stride_b, q_stride_h, out_stride_b, out_stride_h, bt_stride, num_cache_blocks})
       if (x <= -lim || x >= lim) return MIP_EUNSUPPORTED;
@@ -993,7 +999,7 @@ extern "C" size_t mip_paged_decode_plan_bytes(int32_t batch, int32_t num_heads, 
     return 0;
   const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
   if (wl.algo != Algo::kStream) return 0;
-  return static_cast<size_t>(stream_plan_bytes(wl.stream, batch, num_kv_heads));
+  return static_cast<size_t>(stream_plan_bytes(wl.stream, batch, num_kv_heads, block_size, max_blocks_per_seq));
 }
 
 extern "C" int mip_paged_decode_plan(const int32_t* context_lens, const int32_t* block_tables, int64_t bt_stride,
@@ -1006,10 +1012,12 @@ extern "C" int mip_paged_decode_plan(const int32_t* context_lens, const int32_t*
   if (!is_pow2(block_size) || block_size > 4096 || max_blocks_per_seq <= 0 || bt_stride < max_blocks_per_seq)
     return MIP_EINVAL;
   if (static_cast<int64_t>(max_blocks_per_seq) * block_size >= (int64_t{1} << 30)) return MIP_EINVAL;
-  if (!context_lens || !block_tables || !plan || (reinterpret_cast<uintptr_t>(plan) & 3)) return MIP_EINVAL;
+  if (!context_lens || !block_tables || !plan || (reinterpret_cast<uintptr_t>(plan) & 7)) return MIP_EINVAL;
   const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
   if (wl.algo != Algo::kStream) return MIP_EUNSUPPORTED;
-  if (plan_bytes < static_cast<size_t>(stream_plan_bytes(wl.stream, batch, num_kv_heads))) return MIP_EINVAL;
+  const int64_t need = stream_plan_bytes(wl.stream, batch, num_kv_heads, block_size, max_blocks_per_seq);
+  if (need == 0) return MIP_EUNSUPPORTED;
+  if (plan_bytes < static_cast<size_t>(need)) return MIP_EINVAL;
   const int st = stream_plan_launch(wl.stream, context_lens, block_tables, bt_stride, batch, num_kv_heads, block_size,
                                     max_blocks_per_seq, static_cast<int32_t*>(plan), static_cast<hipStream_t>(stream));
   return st == 0 ? MIP_OK : st;

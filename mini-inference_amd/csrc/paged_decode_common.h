@@ -101,6 +101,7 @@ struct StreamArgs {
   // 32-bit copies of the 64-bit strides / sizes of DecodeArgs (the host checks they fit), so
   // the stream kernel's loop state stays within the scalar register file.
   int32_t q_sb, q_sh, out_sb, out_sh, bt_stride, ncb;
+  uint32_t nrows;  // rows of one layer's pool (num_cache_blocks * kv heads * block size)
   int rec_stride;  // floats per record: m[16] | l[16] | acc[group][D]
   int* ws_prefix;  // [batch + 1] tile prefix over sequences (written by workgroup 0)
   float* ws_rec;   // [tw][2][rec_stride]
@@ -113,18 +114,23 @@ struct SShape {
   static constexpr int TILE_BYTES = 16 * D * 2;
 };
 
-// Layout of a stream work plan (int32 words), written once per step by the plan kernel:
-//   [0] T total tiles, [1] W active wavefronts, [2] batch, [3] kv heads, [4..7] unused;
-//   then W wavefront records of kPlanWave words: lo, hi (global tiles), b, kvh, t (start
-//   cursor), L (clamped length of b), nh (block-id hints), h0, h1 (block ids of the first
-//   tiles, block size >= 16 only);
-//   then batch * kv heads segment records of kPlanSeg words: g_lo (first wavefront holding a
-//   piece), R (pieces), lo_split (the first piece sits in that wavefront's "last segment"
-//   slot), L.
+// Layout of a stream work plan (int32 words), written once per step by the plan kernel
+// (block size >= 16 only):
+//   header [kPlanHeader]: T total tiles, W active wavefronts, batch, kv heads, word offset of
+//     the tile descriptors, word offset of the segment records, 0, 0;
+//   W wavefront records of kPlanWave words: lo, hi (global tile range);
+//   batch * kv heads segment records of kPlanSeg words: g_lo (first wavefront holding a piece),
+//     R (pieces), lo_split (the first piece sits in that wavefront's "last segment" slot), L;
+//   T tile descriptors of 2 words (8-byte aligned): the pool row of the tile's first key,
+//     (block * kv heads + kv head) * block size + offset (0xffffffff for a block id outside
+//     the pool), and meta = b | kv head << 16 | valid keys << 24 | first << 29 | last << 30
+//     (first / last: tile 0 / the last tile of its segment).
 constexpr int kPlanHeader = 8;
-constexpr int kPlanWave = 16;
+constexpr int kPlanWave = 2;
 constexpr int kPlanSeg = 4;
-constexpr int kPlanHints = 2;
+constexpr int kPlanTileOffWord = 4;
+constexpr int kPlanSegOffWord = 5;
+constexpr uint32_t kTileNoRow = 0xffffffffu;
 
 __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
 #pragma unroll
@@ -153,8 +159,8 @@ struct StreamConfig {
 StreamConfig stream_config(int dtype, int d, int group, int batch);
 int stream_launch(const StreamConfig& cfg, const StreamArgs& sa, int dtype, int d, int group, int num_kv_heads,
                   int batch, hipStream_t stream);
-// Bytes of a work plan for this launch shape, and the plan kernel (one workgroup).
-int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads);
+// Bytes of a work plan for this launch shape (0: no plan, block size < 16), and the plan kernel.
+int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks);
 int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32_t* block_tables, int64_t bt_stride,
                        int batch, int num_kv_heads, int block_size, int max_blocks, int32_t* plan, hipStream_t stream);
 

@@ -149,7 +149,7 @@ __device__ __forceinline__ bool static_all(F&& f) {
   return true;
 }
 
-template <int DT, int D, int QR, int NS, bool FUSED, bool PLANNED>
+template <int DT, int D, int QR, int NS, bool FUSED>
 __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa) {
   using R = Ring<D, QR>;
   using Ops = MfmaOps<DT>;
@@ -177,72 +177,55 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
   };
   const int gw = blockIdx.x * kSW + w;
   int lo = 0, hi = 0, cb = 0, ckvh = 0, ct = 0, cL = 0;
-  int hint_n = 0, hint0 = 0, hint1 = 0;  // block ids of the first tiles (from a plan)
-  if constexpr (PLANNED) {
-    // ---- work split from the step's plan: this wavefront's range and start cursor.
-    if (gw >= load_uniform_i32(sa.plan + 1)) return;
-    const int32_t* pr = sa.plan + kPlanHeader + static_cast<int64_t>(gw) * kPlanWave;
-    lo = load_uniform_i32(pr + 0);
-    hi = load_uniform_i32(pr + 1);
-    cb = load_uniform_i32(pr + 2);
-    ckvh = load_uniform_i32(pr + 3);
-    ct = load_uniform_i32(pr + 4);
-    cL = load_uniform_i32(pr + 5);
-    hint_n = load_uniform_i32(pr + 6);
-    hint0 = load_uniform_i32(pr + 7);
-    hint1 = load_uniform_i32(pr + 8);
-    if (lo >= hi) return;
-  } else {
-    // ---- work split: context lengths -> tile prefix (block-wide exclusive scan).
-    for (int i = tid; i < B; i += kSW * kWave) {
-      int L = a.lens[i];
-      L = L < cap ? L : cap;
-      s_len[i] = L > 0 ? L : 0;
-    }
-    __syncthreads();
-    {
-      const int chunk = (B + kSW * kWave - 1) / (kSW * kWave);
-      const int beg = tid * chunk < B ? tid * chunk : B;
-      const int end = beg + chunk < B ? beg + chunk : B;
-      int sum = 0;
-      for (int i = beg; i < end; ++i) sum += (s_len[i] + 15) >> 4;
-      const int incl = wave_inclusive_scan(sum, lane);
-      if (lane == kWave - 1) s_wtot[w] = incl;
-      __syncthreads();
-      int off = 0;
-      for (int j = 0; j < w; ++j) off += s_wtot[j];
-      int run = off + incl - sum;
-      for (int i = beg; i < end; ++i) {
-        s_pre[i] = run;
-        run += (s_len[i] + 15) >> 4;
-      }
-      if (tid == kSW * kWave - 1) s_pre[B] = off + incl;
-    }
-    __syncthreads();
-    const int total = a.hkv * s_pre[B];
-    if (blockIdx.x == 0) {
-      for (int i = tid; i <= B; i += kSW * kWave) sa.ws_prefix[i] = s_pre[i];
-    }
-    const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
-    const bool active = total > 0 && gw < tw;
-    if (active) {
-      lo = static_cast<int>(static_cast<int64_t>(gw) * total / tw);
-      hi = static_cast<int>(static_cast<int64_t>(gw + 1) * total / tw);
-      int lb = 0, ub = B - 1;  // largest b with Hkv * P[b] <= lo; its segment is not empty
-      while (lb < ub) {
-        const int mid = (lb + ub + 1) >> 1;
-        if (a.hkv * __builtin_amdgcn_readfirstlane(s_pre[mid]) <= lo) lb = mid; else ub = mid - 1;
-      }
-      cb = lb;
-      const int n = __builtin_amdgcn_readfirstlane((s_len[cb] + 15) >> 4);
-      const int rem = lo - a.hkv * __builtin_amdgcn_readfirstlane(s_pre[cb]);
-      ckvh = rem / n;
-      ct = rem - ckvh * n;
-    }
-    __syncthreads();  // the rings below reuse the scan area
-    if (!active || lo >= hi) return;
-    cL = seq_len(cb);
+  // ---- work split: context lengths -> tile prefix (block-wide exclusive scan).
+  for (int i = tid; i < B; i += kSW * kWave) {
+    int L = a.lens[i];
+    L = L < cap ? L : cap;
+    s_len[i] = L > 0 ? L : 0;
   }
+  __syncthreads();
+  {
+    const int chunk = (B + kSW * kWave - 1) / (kSW * kWave);
+    const int beg = tid * chunk < B ? tid * chunk : B;
+    const int end = beg + chunk < B ? beg + chunk : B;
+    int sum = 0;
+    for (int i = beg; i < end; ++i) sum += (s_len[i] + 15) >> 4;
+    const int incl = wave_inclusive_scan(sum, lane);
+    if (lane == kWave - 1) s_wtot[w] = incl;
+    __syncthreads();
+    int off = 0;
+    for (int j = 0; j < w; ++j) off += s_wtot[j];
+    int run = off + incl - sum;
+    for (int i = beg; i < end; ++i) {
+      s_pre[i] = run;
+      run += (s_len[i] + 15) >> 4;
+    }
+    if (tid == kSW * kWave - 1) s_pre[B] = off + incl;
+  }
+  __syncthreads();
+  const int total = a.hkv * s_pre[B];
+  if (blockIdx.x == 0) {
+    for (int i = tid; i <= B; i += kSW * kWave) sa.ws_prefix[i] = s_pre[i];
+  }
+  const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
+  const bool active = total > 0 && gw < tw;
+  if (active) {
+    lo = static_cast<int>(static_cast<int64_t>(gw) * total / tw);
+    hi = static_cast<int>(static_cast<int64_t>(gw + 1) * total / tw);
+    int lb = 0, ub = B - 1;  // largest b with Hkv * P[b] <= lo; its segment is not empty
+    while (lb < ub) {
+      const int mid = (lb + ub + 1) >> 1;
+      if (a.hkv * __builtin_amdgcn_readfirstlane(s_pre[mid]) <= lo) lb = mid; else ub = mid - 1;
+    }
+    cb = lb;
+    const int n = __builtin_amdgcn_readfirstlane((s_len[cb] + 15) >> 4);
+    const int rem = lo - a.hkv * __builtin_amdgcn_readfirstlane(s_pre[cb]);
+    ckvh = rem / n;
+    ct = rem - ckvh * n;
+  }
+  __syncthreads();  // the rings below reuse the scan area
+  if (!active || lo >= hi) return;
+  cL = seq_len(cb);
   int cn = (cL + 15) >> 4;
   int pb = cb, pkvh = ckvh, pt = ct, pL = cL, pn = cn;  // producer cursor (next tile to load)
   // Fused append: the new token's slot of the producer's sequence, fetched when the producer
@@ -277,16 +260,14 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
 
   uint32_t vmask[NS];  // per stage: bit r = key row r of the tile is a key of its segment
 
-  // hint: the tile's block id when the plan already looked it up (prologue only).
-  auto produce = [&](auto stage_c, auto scalar_table, bool has_hint = false, int hint = 0)
-                     __attribute__((always_inline)) {
+  auto produce = [&](auto stage_c, auto scalar_table) __attribute__((always_inline)) {
     constexpr int s = decltype(stage_c)::value;
     lchar_t* st = ring_ptr + s * R::STAGE;
     const int tb = 16 * pt;
     const int32_t* table = a.bt + static_cast<int64_t>(pb) * sa.bt_stride;
     if constexpr (decltype(scalar_table)::value) {
       // block_size >= 16: the tile lies in one block.
-      const int blk = has_hint ? hint : load_uniform_i32(table + (tb >> a.log2_bs));
+      const int blk = load_uniform_i32(table + (tb >> a.log2_bs));
       const bool bok = blk >= 0 && blk < sa.ncb;
       const int rem = pL - tb;
       const int nvalid = bok ? (rem < 16 ? rem : 16) : 0;
@@ -484,11 +465,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     static_for<0, NS - 1>([&](auto kc) __attribute__((always_inline)) {
       constexpr int k = decltype(kc)::value;
       if constexpr (k > 0) adv_p(lo + k);
-      if constexpr (PLANNED && k < kPlanHints) {
-        produce(ic<k>{}, scalar_table, k < hint_n, k == 0 ? hint0 : hint1);
-      } else {
-        produce(ic<k>{}, scalar_table);
-      }
+      produce(ic<k>{}, scalar_table);
     });
     int i = lo;
 #if MIP_STREAM_PRIO
@@ -496,15 +473,22 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     // ... 0 in its last). The arbiter otherwise favours older wavefronts, so the ones
     // dispatched last on a CU fall behind and finish long after the rest.
     const int span = hi - lo;
-    int quarter = 0;
+    const int q1 = lo + (span + 3) / 4, q2 = lo + (2 * span + 3) / 4, q3 = lo + (3 * span + 3) / 4;
+    int next_q = q1, quarter = 0;
     __builtin_amdgcn_s_setprio(3);
     auto reprioritise = [&]() __attribute__((always_inline)) {
-      const int q = ((i - lo) * 4) / span;
-      if (q == quarter) return;
-      quarter = q;
-      if (q == 1) __builtin_amdgcn_s_setprio(2);
-      else if (q == 2) __builtin_amdgcn_s_setprio(1);
-      else __builtin_amdgcn_s_setprio(0);
+      if (i < next_q) return;
+      ++quarter;
+      if (quarter == 1) {
+        __builtin_amdgcn_s_setprio(2);
+        next_q = q2;
+      } else if (quarter == 2) {
+        __builtin_amdgcn_s_setprio(1);
+        next_q = q3;
+      } else {
+        __builtin_amdgcn_s_setprio(0);
+        next_q = hi;
+      }
     };
 #endif
     // Step on stage k: load tile i+NS-1 into the stage freed last step, then compute tile i.
@@ -527,6 +511,309 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     run(std::true_type{});
   } else {
     run(std::false_type{});
+  }
+  wait_vmcnt<0>();  // no direct load may land in LDS after this wavefront ends
+}
+
+// The stream kernel driven by a work plan (block size >= 16): the same split, ring, tile
+// arithmetic and records as paged_decode_stream, but every tile's pool row, sequence, kv
+// head, valid-key count and segment edges come from the plan's tile descriptors, so the loop
+// does no block-table lookups and no cursor arithmetic. A wavefront holds up to 64 of its
+// descriptors in registers (one per lane, loaded once) and takes each with a lane read.
+template <int DT, int D, int QR, int NS, bool FUSED>
+__global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamArgs sa) {
+  using R = Ring<D, QR>;
+  using Ops = MfmaOps<DT>;
+  using S = typename Elem<DT>::S;
+  constexpr int KC = R::KC, MT = R::MT, RB = R::RB, CPR = R::CPR, RPD = R::RPD;
+  constexpr int RING = NS * R::STAGE;
+  const DecodeArgs& a = sa.a;
+  const int G = sa.group;
+  extern __shared__ __attribute__((aligned(16))) char dsm[];
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int i16 = lane & 15, grp = lane >> 4;
+  const AppendRows& ap = sa.app;
+  const int gw = blockIdx.x * kSW + w;
+  const int32_t* plan = sa.plan;
+  // A plan made for another batch or kv-head count would index past this call's tensors.
+  if (load_uniform_i32(plan + 2) != sa.batch || load_uniform_i32(plan + 3) != a.hkv) return;
+  if (gw >= load_uniform_i32(plan + 1)) return;
+  const int lo = load_uniform_i32(plan + kPlanHeader + kPlanWave * gw);
+  const int hi = load_uniform_i32(plan + kPlanHeader + kPlanWave * gw + 1);
+  if (lo >= hi) return;
+  const uint2* tdesc = reinterpret_cast<const uint2*>(plan + load_uniform_i32(plan + kPlanTileOffWord));
+
+  // ---- descriptors of tiles cbase .. cbase + 63 in registers (lane j holds tile cbase + j).
+  int cbase = lo;
+  uint2 dv = lane < hi - lo ? tdesc[lo + lane] : make_uint2(kTileNoRow, 0u);
+
+  // ---- per-lane LDS addresses (as paged_decode_stream).
+  lchar_t* lds = (lchar_t*)(dsm);
+  lchar_t* ring_ptr = lds + w * RING;
+  const uint32_t ring = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring_ptr));
+  uint32_t k_addr[KC], q_addr[KC];
+  const int qrow = i16 & (QR - 1);
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    const int c = 4 * kc + grp;
+    k_addr[kc] = ring + R::K_OFF + i16 * RB + ((c ^ (i16 & (CPR - 1))) * 16);
+    q_addr[kc] = ring + R::Q_OFF + qrow * RB + ((c ^ (qrow & (CPR - 1))) * 16);
+  }
+  const uint32_t v_addr = ring + R::V_OFF + (4 * grp) * RB + i16 * 2;
+  const int dma_r = lane / CPR, dma_pc = lane % CPR;
+  // Lane offsets inside a tile's rows (row r < valid keys; other rows re-read row 0).
+  uint32_t k_lane[R::KI], v_lane[R::KI];
+  int r_lane[R::KI];
+#pragma unroll
+  for (int j = 0; j < R::KI; ++j) {
+    const int r = j * RPD + dma_r;
+    r_lane[j] = r;
+    k_lane[j] = static_cast<uint32_t>(r * RB + ((dma_pc ^ (r & (CPR - 1))) * 16));
+    v_lane[j] = static_cast<uint32_t>(r * RB + dma_pc * 16);
+  }
+  uint32_t q_lane[R::QI];
+#pragma unroll
+  for (int j = 0; j < R::QI; ++j) {
+    const int hr = j * RPD + dma_r;
+    const int hh = hr < G ? hr : 0;
+    q_lane[j] = static_cast<uint32_t>(hh * sa.q_sh * 2 + ((dma_pc ^ (hr & (CPR - 1))) * 16));
+  }
+
+  uint32_t vmask[NS];  // per stage: bit r = key row r of the tile is a key of its segment
+  uint32_t smeta[NS];  // per stage: the tile's meta word (valid count corrected)
+
+  // Stage tile x: its K and V rows (2 * KI loads), and the q block of its sequence when the
+  // consumer starts a segment there (QI more). Tiles past the range issue nothing; the
+  // consumer's waits cover both (see consume).
+  auto produce = [&](auto stage_c, int x) __attribute__((always_inline)) {
+    constexpr int s = decltype(stage_c)::value;
+    lchar_t* st = ring_ptr + s * R::STAGE;
+    if (x >= hi) return;
+    if (x - cbase >= kWave) {  // next 64 descriptors (long ranges only; drains the loads in flight)
+      cbase = x;
+      dv = x + lane < hi ? tdesc[x + lane] : make_uint2(kTileNoRow, 0u);
+    }
+    const uint32_t row0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(dv.x), x - cbase));
+    uint32_t meta = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(dv.y), x - cbase));
+    const bool ok = row0 < sa.nrows;
+    const int nvalid = ok ? static_cast<int>((meta >> 24) & 31u) : 0;
+    meta = (meta & ~(31u << 24)) | (static_cast<uint32_t>(nvalid) << 24);
+    smeta[s] = meta;
+    vmask[s] = nvalid >= 16 ? 0xffffu : ((1u << nvalid) - 1u);
+    const uint64_t tile_off = static_cast<uint64_t>(ok ? row0 : 0u) * RB;
+    const char* kb = a.k + tile_off;
+    const char* vb = a.v + tile_off;
+    const int b = static_cast<int>(meta & 0xffffu), kvh = static_cast<int>((meta >> 16) & 0xffu);
+    // Fused append: the segment's last tile holds the newest key (position L - 1); when the new
+    // token's slot is that key's slot, its row comes from the new-row source.
+    int nr = -1;
+    if (FUSED && ((meta >> 30) & 1u) && nvalid > 0) {
+      const int64_t slot = load_uniform_i64(ap.slots + b);
+      if (slot >= 0 && (slot >> a.log2_bs) < sa.ncb) {  // then every row index below fits 31 bits
+        const int s32 = static_cast<int>(slot);
+        const int srow = ((s32 >> a.log2_bs) * a.hkv + kvh) * a.bs + (s32 & (a.bs - 1));
+        if (static_cast<uint32_t>(srow) == row0 + static_cast<uint32_t>(nvalid - 1)) nr = nvalid - 1;
+      }
+    }
+    if (FUSED && nr >= 0) {
+      const char* nk = ap.k + static_cast<int64_t>(b) * ap.k_st + static_cast<int64_t>(kvh) * ap.k_sh;
+      const char* nv = ap.v + static_cast<int64_t>(b) * ap.v_st + static_cast<int64_t>(kvh) * ap.v_sh;
+#pragma unroll
+      for (int j = 0; j < R::KI; ++j) {
+        const int r = r_lane[j];
+        const bool fresh = r == nr;
+        const uint32_t ko = r < nvalid ? k_lane[j] : k_lane[j] - static_cast<uint32_t>(r * RB);
+        const uint32_t vo = r < nvalid ? v_lane[j] : v_lane[j] - static_cast<uint32_t>(r * RB);
+        dma16(fresh ? nk + (k_lane[j] - r * RB) : kb + ko, st + R::K_OFF + j * 1024);
+        dma16(fresh ? nv + dma_pc * 16 : vb + vo, st + R::V_OFF + j * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < R::KI; ++j) {
+        const int r = r_lane[j];
+        const uint32_t ko = r < nvalid ? k_lane[j] : k_lane[j] - static_cast<uint32_t>(r * RB);
+        const uint32_t vo = r < nvalid ? v_lane[j] : v_lane[j] - static_cast<uint32_t>(r * RB);
+        dma16(kb + ko, st + R::K_OFF + j * 1024);
+        dma16(vb + vo, st + R::V_OFF + j * 1024);
+      }
+    }
+    if (((meta >> 29) & 1u) || x == lo) {
+      const char* qb = a.q + (static_cast<int64_t>(b) * sa.q_sb + static_cast<int64_t>(kvh * G) * sa.q_sh) * 2;
+#pragma unroll
+      for (int j = 0; j < R::QI; ++j) dma16(qb + q_lane[j], st + R::Q_OFF + j * 1024);
+    }
+  };
+
+  f32x4_t acc[MT];
+  u32x4_t qreg[KC];
+  float m = -INFINITY, l = 0.0f;
+  bool full_start = false;  // the current segment started at its tile 0 in this wavefront
+  bool first_seg = true;    // the current segment holds this wavefront's first tile
+  const bool live = i16 < G;
+  S* out_base = reinterpret_cast<S*>(a.out);
+
+  auto consume = [&](auto stage_c, int i) __attribute__((always_inline)) {
+    constexpr int s = decltype(stage_c)::value;
+    constexpr int SO = s * R::STAGE;
+    // Loads complete in issue order. Every later stage issued at least 2 * KI loads, so at most
+    // (NS - 1) * 2 * KI outstanding means this stage's loads have landed. Near the end of the
+    // range fewer stages follow: wait for everything.
+    if (i + NS - 1 < hi) {
+      wait_vmcnt<(NS - 1) * 2 * R::KI>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    const uint32_t meta = smeta[s];
+    const bool seg_first = (meta >> 29) & 1u, seg_last = (meta >> 30) & 1u;
+    if (seg_first || i == lo) {
+      m = -INFINITY;
+      l = 0.0f;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      full_start = seg_first;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) qreg[kc] = lds_b128<SO>(q_addr[kc]);
+      lgkm_wait();
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) after_wait(qreg[kc]);
+    }
+    const uint32_t vm = vmask[s];
+    u32x4_t kreg[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) kreg[kc] = lds_b128<SO>(k_addr[kc]);
+    uint32_t ve[MT][4];  // V^T operand halves: keys 4*grp + e at dim 16*mt + i16
+    if (vm) {
+      static_for<0, MT>([&](auto mtc) {
+        constexpr int mt = decltype(mtc)::value;
+        ve[mt][0] = lds_u16<SO + 0 * RB + 32 * mt>(v_addr);
+        ve[mt][1] = lds_u16<SO + 1 * RB + 32 * mt>(v_addr);
+        ve[mt][2] = lds_u16<SO + 2 * RB + 32 * mt>(v_addr);
+        ve[mt][3] = lds_u16<SO + 3 * RB + 32 * mt>(v_addr);
+      });
+    }
+    lgkm_wait();
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) after_wait(kreg[kc]);
+    uint32_t vt[MT][2];
+    if (vm) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) after_wait(ve[mt][e]);
+        vt[mt][0] = ve[mt][0] | (ve[mt][1] << 16);
+        vt[mt][1] = ve[mt][2] | (ve[mt][3] << 16);
+      }
+    }
+
+    f32x4_t st = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+      st = Ops::qk(__builtin_bit_cast(uint4, kreg[kc]), __builtin_bit_cast(uint4, qreg[kc]), st);
+    float sv[4];
+    bool need = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = live && ((vm >> (4 * grp + j)) & 1u);
+      sv[j] = ok ? st[j] * a.scale_log2 : -INFINITY;
+      need |= sv[j] > m + kRescaleLog2;
+    }
+    if (__any(need)) {
+      const float mx = max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+      const float mn = fmaxf(m, mx);
+      const float alpha = (m == -INFINITY) ? 0.0f : fast_exp2(m - mn);
+      l *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] *= alpha;
+      m = mn;
+    }
+    if (vm) {
+      uint32_t ph[2], pl[2];
+#pragma unroll
+      for (int j = 0; j < 4; j += 2) {
+        const float p0 = sv[j] == -INFINITY ? 0.0f : fast_exp2(sv[j] - m);
+        const float p1 = sv[j + 1] == -INFINITY ? 0.0f : fast_exp2(sv[j + 1] - m);
+        l += p0 + p1;
+        ph[j / 2] = Ops::pack2(p0, p1);
+        pl[j / 2] = Ops::pack2(p0 - Ops::lo(ph[j / 2]), p1 - Ops::hi(ph[j / 2]));
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint2 va = make_uint2(vt[mt][0], vt[mt][1]);
+        acc[mt] = Ops::pv(va, make_uint2(ph[0], ph[1]), acc[mt]);
+        acc[mt] = Ops::pv(va, make_uint2(pl[0], pl[1]), acc[mt]);
+      }
+    }
+
+    if (seg_last || i == hi - 1) {
+      const float lt = sum4(l);
+      const int b = static_cast<int>(meta & 0xffffu), kvh = static_cast<int>((meta >> 16) & 0xffu);
+      if (full_start && seg_last) {
+        if (live) {
+          const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+          S* orow = out_base + static_cast<int64_t>(b) * sa.out_sb + static_cast<int64_t>(kvh * G + i16) * sa.out_sh;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const uint32_t w0 = Ops::pack2(acc[mt][0] * inv, acc[mt][1] * inv);
+            const uint32_t w1 = Ops::pack2(acc[mt][2] * inv, acc[mt][3] * inv);
+            *reinterpret_cast<uint2*>(orow + 16 * mt + 4 * grp) = make_uint2(w0, w1);
+          }
+        }
+      } else {
+        float* rec = sa.ws_rec + (static_cast<int64_t>(gw) * 2 + (first_seg ? 0 : 1)) * sa.rec_stride;
+        if (live) {
+          if (grp == 0) {
+            rec[i16] = m;
+            rec[16 + i16] = lt;
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            *reinterpret_cast<f32x4_t*>(rec + 32 + i16 * D + 16 * mt + 4 * grp) = acc[mt];
+        }
+      }
+      first_seg = false;
+    }
+  };
+
+  // Prologue: tiles lo .. lo+NS-2 into stages 0 .. NS-2.
+  static_for<0, NS - 1>([&](auto kc) __attribute__((always_inline)) {
+    constexpr int k = decltype(kc)::value;
+    produce(ic<k>{}, lo + k);
+  });
+  int i = lo;
+#if MIP_STREAM_PRIO
+  // Tile indices where the priority drops (the quarters of the range), computed once.
+  const int span = hi - lo;
+  const int q1 = lo + (span + 3) / 4, q2 = lo + (2 * span + 3) / 4, q3 = lo + (3 * span + 3) / 4;
+  int next_q = q1, quarter = 0;
+  __builtin_amdgcn_s_setprio(3);
+  auto reprioritise = [&]() __attribute__((always_inline)) {
+    if (i < next_q) return;
+    ++quarter;
+    if (quarter == 1) {
+      __builtin_amdgcn_s_setprio(2);
+      next_q = q2;
+    } else if (quarter == 2) {
+      __builtin_amdgcn_s_setprio(1);
+      next_q = q3;
+    } else {
+      __builtin_amdgcn_s_setprio(0);
+      next_q = hi;
+    }
+  };
+#endif
+  auto step = [&](auto kc) __attribute__((always_inline)) -> bool {
+    constexpr int k = decltype(kc)::value;
+    produce(ic<(k + NS - 1) % NS>{}, i + NS - 1);
+    consume(ic<k>{}, i);
+    if (++i >= hi) return false;
+#if MIP_STREAM_PRIO
+    reprioritise();
+#endif
+    return true;
+  };
+  while (static_all<0, NS>(step)) {
   }
   wait_vmcnt<0>();  // no direct load may land in LDS after this wavefront ends
 }
@@ -559,8 +846,7 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
   int L, gw_lo, gw_hi;
   bool lo_split;
   if constexpr (PLANNED) {
-    const int W = load_uniform_i32(sa.plan + 1);
-    const int32_t* sd = sa.plan + kPlanHeader + static_cast<int64_t>(W) * kPlanWave +
+    const int32_t* sd = sa.plan + load_uniform_i32(sa.plan + kPlanSegOffWord) +
                         (static_cast<int64_t>(b) * a.hkv + kvh) * kPlanSeg;
     gw_lo = load_uniform_i32(sd + 0);
     gw_hi = gw_lo + load_uniform_i32(sd + 1) - 1;
@@ -677,11 +963,12 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
   }
 }
 
-// ---- the per-step work plan (mip_paged_decode_plan): one workgroup computes, from the
-// context lengths and block tables, the split the stream kernel would otherwise derive in
-// every call: wavefront ranges and start cursors, the first tiles' block ids, and every
-// segment's merge descriptor. Layout: kPlanHeader / kPlanWave / kPlanSeg.
-constexpr int kPlanThreads = 1024;
+// ---- the per-step work plan (mip_paged_decode_plan): computed once per decode step from the
+// context lengths and block tables, shared by every layer's call. Every workgroup scans the
+// lengths into the tile prefix (cheap: at most 4096 sequences), then the grid writes, in
+// grid-stride loops, the wavefront ranges, the segment records for the merge kernel and one
+// descriptor per tile. Layout: kPlanHeader / kPlanWave / kPlanSeg / tile descriptors.
+constexpr int kPlanThreads = 256;
 
 struct PlanArgs {
   const int32_t* lens;
@@ -689,6 +976,7 @@ struct PlanArgs {
   int64_t bt_stride;
   int32_t* plan;
   int batch, hkv, bs, log2_bs, cap, tw, min_tiles;
+  int seg_off, tile_off;  // word offsets of the segment records and tile descriptors
 };
 
 __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArgs p) {
@@ -725,58 +1013,23 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArg
   __syncthreads();
   const int64_t T = static_cast<int64_t>(p.hkv) * s_pre[B];
   const int W = T > 0 ? stream_active_waves(p.tw, static_cast<int>(T), p.min_tiles) : 0;
-  if (tid == 0) {
+  const int gtid = blockIdx.x * kPlanThreads + tid, gstride = gridDim.x * kPlanThreads;
+  if (gtid == 0) {
     p.plan[0] = static_cast<int32_t>(T);
     p.plan[1] = W;
     p.plan[2] = B;
     p.plan[3] = p.hkv;
+    p.plan[kPlanTileOffWord] = p.tile_off;
+    p.plan[kPlanSegOffWord] = p.seg_off;
   }
-  // Wavefront records: the same split and cursor arithmetic as the in-kernel path.
-  for (int g = tid; g < W; g += kPlanThreads) {
-    const int lo = static_cast<int>(static_cast<int64_t>(g) * T / W);
-    const int hi = static_cast<int>(static_cast<int64_t>(g + 1) * T / W);
-    int lb = 0, ub = B - 1;  // largest b with Hkv * P[b] <= lo
-    while (lb < ub) {
-      const int mid = (lb + ub + 1) >> 1;
-      if (p.hkv * s_pre[mid] <= lo) lb = mid; else ub = mid - 1;
-    }
-    int b = lb, L = s_len[b], n = (L + 15) >> 4;
-    const int rem = lo - p.hkv * s_pre[b];
-    int kvh = rem / n, t = rem - kvh * n;
+  // Wavefront ranges: the same split as the in-kernel path.
+  for (int g = gtid; g < W; g += gstride) {
     int32_t* r = p.plan + kPlanHeader + static_cast<int64_t>(g) * kPlanWave;
-    r[0] = lo;
-    r[1] = hi;
-    r[2] = b;
-    r[3] = kvh;
-    r[4] = t;
-    r[5] = L;
-    // Block ids of the first tiles the producer stages (block size >= 16 only: then a tile
-    // lies in one block). The cursor moves exactly as the stream kernel's producer does.
-    int nh = 0;
-    if (p.bs >= 16) {
-      for (int k = 0; k < kPlanHints; ++k) {
-        if (k > 0 && lo + k < hi) {
-          if (++t >= n) {
-            t = 0;
-            if (++kvh >= p.hkv) {
-              kvh = 0;
-              do {
-                ++b;
-                L = b < B ? s_len[b] : 16;
-                n = (L + 15) >> 4;
-              } while (n == 0);
-            }
-          }
-        }
-        r[7 + k] = p.bt[static_cast<int64_t>(b) * p.bt_stride + ((16 * t) >> p.log2_bs)];
-        ++nh;
-      }
-    }
-    r[6] = nh;
+    r[0] = static_cast<int>(static_cast<int64_t>(g) * T / W);
+    r[1] = static_cast<int>(static_cast<int64_t>(g + 1) * T / W);
   }
   // Segment records for the merge kernel.
-  int32_t* seg = p.plan + kPlanHeader + static_cast<int64_t>(W) * kPlanWave;
-  for (int sidx = tid; sidx < B * p.hkv; sidx += kPlanThreads) {
+  for (int sidx = gtid; sidx < B * p.hkv; sidx += gstride) {
     const int b = sidx / p.hkv, kvh = sidx - b * p.hkv;
     const int L = s_len[b], n = (L + 15) >> 4;
     int g_lo = 0, R = 0, lo_split = 0;
@@ -788,11 +1041,32 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArg
       R = g_hi - g_lo + 1;
       lo_split = static_cast<int64_t>(g_lo) * T / W < s0 ? 1 : 0;
     }
-    int32_t* r = seg + static_cast<int64_t>(sidx) * kPlanSeg;
+    int32_t* r = p.plan + p.seg_off + static_cast<int64_t>(sidx) * kPlanSeg;
     r[0] = g_lo;
     r[1] = R;
     r[2] = lo_split;
     r[3] = L;
+  }
+  // Tile descriptors: tile x of the global sequence (sequence-major, then kv head, then key tile).
+  uint2* td = reinterpret_cast<uint2*>(p.plan + p.tile_off);
+  for (int64_t x = gtid; x < T; x += gstride) {
+    int lb = 0, ub = B - 1;  // largest b with Hkv * P[b] <= x; its segment is not empty
+    while (lb < ub) {
+      const int mid = (lb + ub + 1) >> 1;
+      if (static_cast<int64_t>(p.hkv) * s_pre[mid] <= x) lb = mid; else ub = mid - 1;
+    }
+    const int b = lb, L = s_len[b], n = (L + 15) >> 4;
+    const int rem = static_cast<int>(x - static_cast<int64_t>(p.hkv) * s_pre[b]);
+    const int kvh = rem / n, t = rem - kvh * n;
+    const int tb = 16 * t;
+    const int blk = p.bt[static_cast<int64_t>(b) * p.bt_stride + (tb >> p.log2_bs)];
+    const int64_t row = (static_cast<int64_t>(blk) * p.hkv + kvh) * p.bs + (tb & (p.bs - 1));
+    const uint32_t row0 = (blk < 0 || row >= static_cast<int64_t>(kTileNoRow)) ? kTileNoRow : static_cast<uint32_t>(row);
+    const int nvalid = L - tb < 16 ? L - tb : 16;
+    const uint32_t meta = static_cast<uint32_t>(b) | (static_cast<uint32_t>(kvh) << 16) |
+                          (static_cast<uint32_t>(nvalid) << 24) | (t == 0 ? 1u << 29 : 0u) |
+                          (t == n - 1 ? 1u << 30 : 0u);
+    td[x] = make_uint2(row0, meta);
   }
 }
 
@@ -808,10 +1082,10 @@ template <int DT, int D, int QR>
 StreamPick pick_one() {
   constexpr int NS = D == 64 ? MIP_STREAM_STAGES_D64 : MIP_STREAM_STAGES_D128;
   StreamPick p;
-  p.main[0][0] = paged_decode_stream<DT, D, QR, NS, false, false>;
-  p.main[0][1] = paged_decode_stream<DT, D, QR, NS, false, true>;
-  p.main[1][0] = paged_decode_stream<DT, D, QR, NS, true, false>;
-  p.main[1][1] = paged_decode_stream<DT, D, QR, NS, true, true>;
+  p.main[0][0] = paged_decode_stream<DT, D, QR, NS, false>;
+  p.main[0][1] = paged_decode_stream_tiles<DT, D, QR, NS, false>;
+  p.main[1][0] = paged_decode_stream<DT, D, QR, NS, true>;
+  p.main[1][1] = paged_decode_stream_tiles<DT, D, QR, NS, true>;
   p.merge[0][0] = paged_decode_stream_merge<DT, D, false, false>;
   p.merge[0][1] = paged_decode_stream_merge<DT, D, false, true>;
   p.merge[1][0] = paged_decode_stream_merge<DT, D, true, false>;
@@ -876,14 +1150,34 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, i
   return static_cast<int>(hipGetLastError());
 }
 
-int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads) {
-  return (kPlanHeader + static_cast<int64_t>(cfg.tw) * kPlanWave +
-          static_cast<int64_t>(batch) * num_kv_heads * kPlanSeg) * 4;
+namespace {
+struct PlanLayout {
+  int64_t seg_off, tile_off, words;
+};
+PlanLayout plan_layout(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks) {
+  PlanLayout l{};
+  const int64_t tiles_per_seq = (static_cast<int64_t>(max_blocks) * block_size + 15) / 16;
+  l.seg_off = kPlanHeader + static_cast<int64_t>(cfg.tw) * kPlanWave;
+  l.tile_off = l.seg_off + static_cast<int64_t>(batch) * num_kv_heads * kPlanSeg;
+  l.tile_off += l.tile_off & 1;  // descriptors are 8-byte pairs
+  l.words = l.tile_off + 2 * static_cast<int64_t>(batch) * num_kv_heads * tiles_per_seq;
+  return l;
+}
+}  // namespace
+
+int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks) {
+  // Tile descriptors hold one pool row per tile, so a tile must lie in one block; the
+  // descriptor's meta word holds the sequence and kv head in 16 and 8 bits.
+  if (block_size < 16 || batch > 65535 || num_kv_heads > 255) return 0;
+  const PlanLayout l = plan_layout(cfg, batch, num_kv_heads, block_size, max_blocks);
+  if (l.words >= (int64_t{1} << 31)) return 0;
+  return l.words * 4;
 }
 
 int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32_t* block_tables, int64_t bt_stride,
                        int batch, int num_kv_heads, int block_size, int max_blocks, int32_t* plan,
                        hipStream_t stream) {
+  const PlanLayout l = plan_layout(cfg, batch, num_kv_heads, block_size, max_blocks);
   PlanArgs p{};
   p.lens = lens;
   p.bt = block_tables;
@@ -896,8 +1190,14 @@ int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32
   p.cap = max_blocks * block_size;
   p.tw = cfg.tw;
   p.min_tiles = stream_min_tiles();
+  p.seg_off = static_cast<int>(l.seg_off);
+  p.tile_off = static_cast<int>(l.tile_off);
+  // Enough workgroups for about eight descriptors per thread at the largest tile count.
+  const int64_t max_tiles = (l.words - l.tile_off) / 2;
+  int64_t grid = (max_tiles + 8 * kPlanThreads - 1) / (8 * kPlanThreads);
+  grid = grid < 1 ? 1 : (grid > 1024 ? 1024 : grid);
   const size_t lds = static_cast<size_t>(2 * batch + 1 + kPlanThreads / kWave) * 4;
-  hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), lds, stream, p);
+  hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(static_cast<unsigned>(grid)), dim3(kPlanThreads), lds, stream, p);
   return static_cast<int>(hipGetLastError());
 }
 
