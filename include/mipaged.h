@@ -1,12 +1,16 @@
 /*
  * mipaged.h — C ABI of the MI355X paged KV-cache kernels (gfx950).
  *
- * Three operations sit behind this boundary:
- *   1. KV append          : scatter new K/V rows into the paged pool through a slot mapping.
+ * Operations behind this boundary:
+ *   1. KV append          : scatter new K/V rows into the paged pool through a slot mapping
+ *                           (optionally fused with the rotary embedding of q and k).
  *   2. Paged decode attn  : one query token per sequence, GQA, reading K/V pages in place
- *                           through per-sequence block tables.
+ *                           through per-sequence block tables (optionally fused with the
+ *                           append, and driven by a per-step work plan).
  *   3. Block copy         : copy whole blocks (all layers, K and V) for copy-on-write of
  *                           shared prefix blocks.
+ *   4. Paged prefill attn : packed new tokens of several sequences over their cached
+ *                           prefixes and themselves, causal, reading K/V pages in place.
  *
  * Pool layout (one layer; identical to the reference pool
  * engine/kv_cache.py:426-428, `k, v: [num_layers, num_blocks + 1, num_kv_heads,
@@ -135,8 +139,9 @@ int mip_rope_kv_append(void* q, int64_t q_stride_tok, int64_t q_stride_head,
  *
  * `plan` (may be NULL) is a work plan made by mip_paged_decode_plan from the same
  * context_lens and block_tables contents and the same shape, earlier on the stream; the
- * kernel then starts from it instead of deriving its work split itself (every layer of a
- * decode step shares one plan). It is ignored where the stream kernel does not run.
+ * kernel then streams from its tile descriptors instead of deriving its work split and
+ * walking the block tables (every layer of a decode step shares one plan). It is ignored
+ * where the stream kernel does not run and for block_size < 16.
  */
 int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h,
                      const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -183,14 +188,17 @@ int mip_paged_decode_append(const void* k_new, const void* v_new,
  * reference derives nothing per step beyond PagedDecodeContext's tensors,
  * engine/kv_cache.py:592-609).
  *
- * Every layer of a step attends the same sequences, so the stream kernel's work split
- * (each wavefront's range of key tiles and start position, the first tiles' block ids,
- * and which pieces the merge combines) is the same for all of them. One launch of a single
- * workgroup writes it; pass the plan to each layer's mip_paged_decode /
- * mip_paged_decode_append, which then skip that work. Returns MIP_EUNSUPPORTED (nothing
- * launched) for shapes the stream kernel does not run; mip_paged_decode_plan_bytes returns
- * 0 for those. The plan is int32 data, 4-byte aligned, and stays valid while
- * context_lens, block_tables and the shape do not change.
+ * Every layer of a step attends the same sequences, so the stream kernel's work split is
+ * the same for all of them: each wavefront's range of 16-key tiles, which pieces the merge
+ * combines, and one descriptor per tile (its pool row, sequence, kv head, valid keys and
+ * segment edges, read through the block tables once). One launch writes it; pass the plan
+ * to each layer's mip_paged_decode / mip_paged_decode_append, which then stream from the
+ * descriptors instead of walking the block tables. Returns MIP_EUNSUPPORTED (nothing
+ * launched) for shapes the stream kernel does not run and for block_size < 16 (a tile must
+ * lie in one block); mip_paged_decode_plan_bytes returns 0 for those. The plan buffer must
+ * be 8-byte aligned; it holds int32 data and stays valid while context_lens, block_tables
+ * and the shape do not change. A plan made for another batch size or kv-head count is
+ * ignored by the decode kernel (nothing is computed).
  */
 size_t mip_paged_decode_plan_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_dim, int32_t block_size,
