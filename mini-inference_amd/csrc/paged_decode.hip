@@ -907,6 +907,9 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
                           q_stride_h >= 0 && q_stride_h * 2 * 16 < (int64_t{1} << 31);
     if (plan && (reinterpret_cast<uintptr_t>(plan) & 7)) return MIP_EINVAL;
     sa.plan = use_plan ? static_cast<const int32_t*>(plan) : nullptr;
+    if (use_plan)
+      stream_plan_offsets(wl.stream, batch, num_kv_heads, block_size, max_blocks_per_seq, &sa.plan_seg_off,
+                          &sa.plan_tile_off);
     sa.nrows = static_cast<uint32_t>(num_cache_blocks * num_kv_heads * block_size);
     const int64_t lim = int64_t{1} << 31;
     for (const int64_t x : {q_stride_b, q_stride_h, out_stride_b, out_stride_h, bt_stride, num_cache_blocks})

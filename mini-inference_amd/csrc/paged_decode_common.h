@@ -102,6 +102,7 @@ struct StreamArgs {
   // the stream kernel's loop state stays within the scalar register file.
   int32_t q_sb, q_sh, out_sb, out_sh, bt_stride, ncb;
   uint32_t nrows;  // rows of one layer's pool (num_cache_blocks * kv heads * block size)
+  int32_t plan_seg_off, plan_tile_off;  // word offsets of the plan's segment records / tile descriptors
   int rec_stride;  // floats per record: m[16] | l[16] | acc[group][D]
   int* ws_prefix;  // [batch + 1] tile prefix over sequences (written by workgroup 0)
   float* ws_rec;   // [tw][2][rec_stride]
@@ -161,6 +162,9 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa, int dtype, int 
                   int batch, hipStream_t stream);
 // Bytes of a work plan for this launch shape (0: no plan, block size < 16), and the plan kernel.
 int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks);
+// Word offsets of a plan's segment records and tile descriptors (the same the plan kernel writes).
+void stream_plan_offsets(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks,
+                         int32_t* seg_off, int32_t* tile_off);
 int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32_t* block_tables, int64_t bt_stride,
                        int batch, int num_kv_heads, int block_size, int max_blocks, int32_t* plan, hipStream_t stream);
 

@@ -537,13 +537,14 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
   const AppendRows& ap = sa.app;
   const int gw = blockIdx.x * kSW + w;
   const int32_t* plan = sa.plan;
-  // A plan made for another batch or kv-head count would index past this call's tensors.
-  if (load_uniform_i32(plan + 2) != sa.batch || load_uniform_i32(plan + 3) != a.hkv) return;
-  if (gw >= load_uniform_i32(plan + 1)) return;
+  // All plan words this wavefront needs are read before any of them is tested, so their
+  // latencies overlap. (The wavefront record of a wavefront past W is inside the plan too.)
+  const int pw = load_uniform_i32(plan + 1), pb = load_uniform_i32(plan + 2), ph = load_uniform_i32(plan + 3);
   const int lo = load_uniform_i32(plan + kPlanHeader + kPlanWave * gw);
   const int hi = load_uniform_i32(plan + kPlanHeader + kPlanWave * gw + 1);
-  if (lo >= hi) return;
-  const uint2* tdesc = reinterpret_cast<const uint2*>(plan + load_uniform_i32(plan + kPlanTileOffWord));
+  // A plan made for another batch or kv-head count would index past this call's tensors.
+  if (pb != sa.batch || ph != a.hkv || gw >= pw || lo >= hi) return;
+  const uint2* tdesc = reinterpret_cast<const uint2*>(plan + sa.plan_tile_off);
 
   // ---- descriptors of tiles cbase .. cbase + 63 in registers (lane j holds tile cbase + j).
   int cbase = lo;
@@ -846,8 +847,7 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
   int L, gw_lo, gw_hi;
   bool lo_split;
   if constexpr (PLANNED) {
-    const int32_t* sd = sa.plan + load_uniform_i32(sa.plan + kPlanSegOffWord) +
-                        (static_cast<int64_t>(b) * a.hkv + kvh) * kPlanSeg;
+    const int32_t* sd = sa.plan + sa.plan_seg_off + (static_cast<int64_t>(b) * a.hkv + kvh) * kPlanSeg;
     gw_lo = load_uniform_i32(sd + 0);
     gw_hi = gw_lo + load_uniform_i32(sd + 1) - 1;
     lo_split = load_uniform_i32(sd + 2) != 0;
@@ -1172,6 +1172,13 @@ int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads, 
   const PlanLayout l = plan_layout(cfg, batch, num_kv_heads, block_size, max_blocks);
   if (l.words >= (int64_t{1} << 31)) return 0;
   return l.words * 4;
+}
+
+void stream_plan_offsets(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks,
+                         int32_t* seg_off, int32_t* tile_off) {
+  const PlanLayout l = plan_layout(cfg, batch, num_kv_heads, block_size, max_blocks);
+  *seg_off = static_cast<int32_t>(l.seg_off);
+  *tile_off = static_cast<int32_t>(l.tile_off);
 }
 
 int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32_t* block_tables, int64_t bt_stride,
