@@ -336,7 +336,7 @@ def main() -> int:
         "frac_of_peak": round(value / HBM_PEAK_GBPS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_stream<bf16, D=64, QR=8, NS=3> (with the fused append) + "
+            "kernel": "paged_decode_stream_tiles<bf16, D=64, QR=8, NS=3> (planned, with the fused append) + "
                       "paged_decode_stream_merge<bf16, D=64>",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
