@@ -140,8 +140,10 @@ int mip_rope_kv_append(void* q, int64_t q_stride_tok, int64_t q_stride_head,
  * `plan` (may be NULL) is a work plan made by mip_paged_decode_plan from the same
  * context_lens and block_tables contents and the same shape, earlier on the stream; the
  * kernel then streams from its tile descriptors instead of deriving its work split and
- * walking the block tables (every layer of a decode step shares one plan). It is ignored
- * where the stream kernel does not run and for block_size < 16.
+ * walking the block tables (every layer of a decode step shares one plan). `plan_bytes` is
+ * the size of the plan buffer: below mip_paged_decode_plan_bytes for this shape it is
+ * MIP_EINVAL. The plan is ignored where the stream kernel does not run and for
+ * block_size < 16.
  */
 int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h,
                      const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -151,7 +153,7 @@ int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h,
                      int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                      int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
                      float scale, void* workspace, size_t workspace_bytes,
-                     const void* plan, int32_t dtype, void* stream);
+                     const void* plan, size_t plan_bytes, int32_t dtype, void* stream);
 
 /*
  * KV append + paged decode attention in one call: the whole of
@@ -181,7 +183,7 @@ int mip_paged_decode_append(const void* k_new, const void* v_new,
                             int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                             int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
                             float scale, void* workspace, size_t workspace_bytes,
-                            const void* plan, int32_t dtype, void* stream);
+                            const void* plan, size_t plan_bytes, int32_t dtype, void* stream);
 
 /*
  * Work plan of the decode kernels for one decode step (no reference counterpart: the

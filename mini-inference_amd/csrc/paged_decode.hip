@@ -833,7 +833,7 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
                       const int32_t* block_tables, int64_t bt_stride, const int32_t* context_lens, int32_t batch,
                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                       int32_t max_blocks_per_seq, float scale, void* workspace, size_t workspace_bytes,
-                      const void* plan, int32_t dtype, void* stream, const AppendRows& app) {
+                      const void* plan, size_t plan_bytes, int32_t dtype, void* stream, const AppendRows& app) {
   if (dtype != MIP_F32 && dtype != MIP_F16 && dtype != MIP_BF16) return MIP_EINVAL;
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return MIP_EINVAL;
   if (num_heads % num_kv_heads != 0) return MIP_EINVAL;
@@ -902,14 +902,16 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
     sa.app = app;
     // A plan drives the tile-descriptor kernel, which needs tiles inside one block and 32-bit
     // lane offsets into the q head rows; otherwise the kernel derives its split itself.
-    const bool use_plan = plan != nullptr && stream_plan_bytes(wl.stream, batch, num_kv_heads, block_size,
-                                                               max_blocks_per_seq) > 0 &&
-                          q_stride_h >= 0 && q_stride_h * 2 * 16 < (int64_t{1} << 31);
+    const int64_t plan_need = stream_plan_bytes(wl.stream, batch, num_kv_heads, block_size, max_blocks_per_seq);
+    const bool use_plan = plan != nullptr && plan_need > 0 && q_stride_h >= 0 &&
+                          q_stride_h * 2 * 16 < (int64_t{1} << 31);
     if (plan && (reinterpret_cast<uintptr_t>(plan) & 7)) return MIP_EINVAL;
+    // The kernel reads the plan at offsets of this shape's layout before it checks the header.
+    if (use_plan && plan_bytes < static_cast<size_t>(plan_need)) return MIP_EINVAL;
     sa.plan = use_plan ? static_cast<const int32_t*>(plan) : nullptr;
     if (use_plan)
       stream_plan_offsets(wl.stream, batch, num_kv_heads, block_size, max_blocks_per_seq, &sa.plan_seg_off,
-                          &sa.plan_tile_off);
+                          &sa.plan_tile_off, &sa.plan_wave_cap);
     sa.nrows = static_cast<uint32_t>(num_cache_blocks * num_kv_heads * block_size);
     const int64_t lim = int64_t{1} << 31;
     for (const int64_t x : {q_stride_b, q_stride_h, out_stride_b, out_stride_h, bt_stride, num_cache_blocks})
@@ -936,12 +938,12 @@ extern "C" int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_str
                                 int64_t num_cache_blocks, const int32_t* block_tables, int64_t bt_stride,
                                 const int32_t* context_lens, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                 int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq, float scale,
-                                void* workspace, size_t workspace_bytes, const void* plan, int32_t dtype,
-                                void* stream) {
+                                void* workspace, size_t workspace_bytes, const void* plan, size_t plan_bytes,
+                                int32_t dtype, void* stream) {
   return paged_decode_impl(out, out_stride_b, out_stride_h, q, q_stride_b, q_stride_h, k_cache, v_cache,
                            num_cache_blocks, block_tables, bt_stride, context_lens, batch, num_heads, num_kv_heads,
-                           head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, plan, dtype,
-                           stream, AppendRows{});
+                           head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, plan,
+                           plan_bytes, dtype, stream, AppendRows{});
 }
 
 extern "C" int mip_paged_decode_append(const void* k_new, const void* v_new, int64_t k_stride_tok,
@@ -952,7 +954,8 @@ extern "C" int mip_paged_decode_append(const void* k_new, const void* v_new, int
                                        const int32_t* block_tables, int64_t bt_stride, const int32_t* context_lens,
                                        int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                        int32_t block_size, int32_t max_blocks_per_seq, float scale, void* workspace,
-                                       size_t workspace_bytes, const void* plan, int32_t dtype, void* stream) {
+                                       size_t workspace_bytes, const void* plan, size_t plan_bytes, int32_t dtype,
+                                       void* stream) {
   if (dtype != MIP_F32 && dtype != MIP_F16 && dtype != MIP_BF16) return MIP_EINVAL;
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return MIP_EINVAL;
   if (batch == 0) return MIP_OK;
@@ -981,7 +984,7 @@ extern "C" int mip_paged_decode_append(const void* k_new, const void* v_new, int
     return paged_decode_impl(out, out_stride_b, out_stride_h, q, q_stride_b, q_stride_h, k_cache, v_cache,
                              num_cache_blocks, block_tables, bt_stride, context_lens, batch, num_heads,
                              num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, workspace,
-                             workspace_bytes, plan, dtype, stream, app);
+                             workspace_bytes, plan, plan_bytes, dtype, stream, app);
   }
   // Not fusable here: the append kernel, then the decode, in stream order.
   const int st = mip_kv_append(k_new, v_new, k_stride_tok, k_stride_head, v_stride_tok, v_stride_head, k_cache,
@@ -990,8 +993,8 @@ extern "C" int mip_paged_decode_append(const void* k_new, const void* v_new, int
   if (st != MIP_OK) return st;
   return mip_paged_decode(out, out_stride_b, out_stride_h, q, q_stride_b, q_stride_h, k_cache, v_cache,
                           num_cache_blocks, block_tables, bt_stride, context_lens, batch, num_heads, num_kv_heads,
-                          head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, plan, dtype,
-                          stream);
+                          head_dim, block_size, max_blocks_per_seq, scale, workspace, workspace_bytes, plan,
+                          plan_bytes, dtype, stream);
 }
 
 extern "C" size_t mip_paged_decode_plan_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,

@@ -103,6 +103,7 @@ struct StreamArgs {
   int32_t q_sb, q_sh, out_sb, out_sh, bt_stride, ncb;
   uint32_t nrows;  // rows of one layer's pool (num_cache_blocks * kv heads * block size)
   int32_t plan_seg_off, plan_tile_off;  // word offsets of the plan's segment records / tile descriptors
+  int32_t plan_wave_cap;                // descriptor slots per wavefront in the plan
   int rec_stride;  // floats per record: m[16] | l[16] | acc[group][D]
   int* ws_prefix;  // [batch + 1] tile prefix over sequences (written by workgroup 0)
   float* ws_rec;   // [tw][2][rec_stride]
@@ -118,19 +119,25 @@ struct SShape {
 // Layout of a stream work plan (int32 words), written once per step by the plan kernel
 // (block size >= 16 only):
 //   header [kPlanHeader]: T total tiles, W active wavefronts, batch, kv heads, word offset of
-//     the tile descriptors, word offset of the segment records, 0, 0;
-//   W wavefront records of kPlanWave words: lo, hi (global tile range);
+//     the tile descriptors, word offset of the segment records, C descriptor slots per
+//     wavefront, 0;
+//   tw wavefront records of kPlanWave words (the first W written): lo, hi (global tile range);
 //   batch * kv heads segment records of kPlanSeg words: g_lo (first wavefront holding a piece),
 //     R (pieces), lo_split (the first piece sits in that wavefront's "last segment" slot), L;
-//   T tile descriptors of 2 words (8-byte aligned): the pool row of the tile's first key,
-//     (block * kv heads + kv head) * block size + offset (0xffffffff for a block id outside
-//     the pool), and meta = b | kv head << 16 | valid keys << 24 | first << 29 | last << 30
-//     (first / last: tile 0 / the last tile of its segment).
+//   tw * C + kWave tile descriptor slots of 2 words (8-byte aligned), wavefront-major: tile x
+//     of wavefront g's range [lo, hi) sits in slot g * C + (x - lo), so a wavefront finds its
+//     first descriptors without reading lo first; C >= hi - lo for every wavefront, and the
+//     kWave spare slots keep a wavefront's 64-slot window inside the plan. A descriptor is
+//     the pool row of the tile's first key, (block * kv heads + kv head) * block size + offset
+//     (0xffffffff for a block id outside the pool), and meta = b | kv head << 16 |
+//     valid keys << 24 | first << 29 | last << 30 (first / last: tile 0 / the last tile of its
+//     segment).
 constexpr int kPlanHeader = 8;
 constexpr int kPlanWave = 2;
 constexpr int kPlanSeg = 4;
 constexpr int kPlanTileOffWord = 4;
 constexpr int kPlanSegOffWord = 5;
+constexpr int kPlanWaveCapWord = 6;
 constexpr uint32_t kTileNoRow = 0xffffffffu;
 
 __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
@@ -162,9 +169,10 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa, int dtype, int 
                   int batch, hipStream_t stream);
 // Bytes of a work plan for this launch shape (0: no plan, block size < 16), and the plan kernel.
 int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks);
-// Word offsets of a plan's segment records and tile descriptors (the same the plan kernel writes).
+// Word offsets of a plan's segment records and tile descriptors, and its descriptor slots per
+// wavefront (the same the plan kernel writes).
 void stream_plan_offsets(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks,
-                         int32_t* seg_off, int32_t* tile_off);
+                         int32_t* seg_off, int32_t* tile_off, int32_t* wave_cap);
 int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32_t* block_tables, int64_t bt_stride,
                        int batch, int num_kv_heads, int block_size, int max_blocks, int32_t* plan, hipStream_t stream);
 

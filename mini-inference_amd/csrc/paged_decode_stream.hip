@@ -539,16 +539,22 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
   const int32_t* plan = sa.plan;
   // All plan words this wavefront needs are read before any of them is tested, so their
   // latencies overlap. (The wavefront record of a wavefront past W is inside the plan too.)
+  // This wavefront's descriptor slots start at a fixed place, so its first 64 descriptors
+  // are read together with its range instead of after it.
+  const uint2* tdesc = reinterpret_cast<const uint2*>(plan + sa.plan_tile_off) +
+                       static_cast<int64_t>(gw) * sa.plan_wave_cap;
   const int pw = load_uniform_i32(plan + 1), pb = load_uniform_i32(plan + 2), ph = load_uniform_i32(plan + 3);
+  const int pt = load_uniform_i32(plan + kPlanTileOffWord), pc = load_uniform_i32(plan + kPlanWaveCapWord);
   const int lo = load_uniform_i32(plan + kPlanHeader + kPlanWave * gw);
   const int hi = load_uniform_i32(plan + kPlanHeader + kPlanWave * gw + 1);
-  // A plan made for another batch or kv-head count would index past this call's tensors.
-  if (pb != sa.batch || ph != a.hkv || gw >= pw || lo >= hi) return;
-  const uint2* tdesc = reinterpret_cast<const uint2*>(plan + sa.plan_tile_off);
+  uint2 dv = tdesc[lane];
+  // A plan made for another batch, kv-head count or layout would index past this call's tensors.
+  if (pb != sa.batch || ph != a.hkv || pt != sa.plan_tile_off || pc != sa.plan_wave_cap || gw >= pw || lo >= hi)
+    return;
 
   // ---- descriptors of tiles cbase .. cbase + 63 in registers (lane j holds tile cbase + j).
   int cbase = lo;
-  uint2 dv = lane < hi - lo ? tdesc[lo + lane] : make_uint2(kTileNoRow, 0u);
+  if (lane >= hi - lo) dv = make_uint2(kTileNoRow, 0u);
 
   // ---- per-lane LDS addresses (as paged_decode_stream).
   lchar_t* lds = (lchar_t*)(dsm);
@@ -594,7 +600,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
     if (x >= hi) return;
     if (x - cbase >= kWave) {  // next 64 descriptors (long ranges only; drains the loads in flight)
       cbase = x;
-      dv = x + lane < hi ? tdesc[x + lane] : make_uint2(kTileNoRow, 0u);
+      dv = x + lane < hi ? tdesc[x - lo + lane] : make_uint2(kTileNoRow, 0u);
     }
     const uint32_t row0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(dv.x), x - cbase));
     uint32_t meta = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(dv.y), x - cbase));
@@ -848,10 +854,14 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
   bool lo_split;
   if constexpr (PLANNED) {
     const int32_t* sd = sa.plan + sa.plan_seg_off + (static_cast<int64_t>(b) * a.hkv + kvh) * kPlanSeg;
+    const int pb = load_uniform_i32(sa.plan + 2), ph = load_uniform_i32(sa.plan + 3);
+    const int ps = load_uniform_i32(sa.plan + kPlanSegOffWord);
     gw_lo = load_uniform_i32(sd + 0);
     gw_hi = gw_lo + load_uniform_i32(sd + 1) - 1;
     lo_split = load_uniform_i32(sd + 2) != 0;
     L = load_uniform_i32(sd + 3);
+    // The main kernel computed nothing with a plan of another shape; its records stay unread.
+    if (pb != sa.batch || ph != a.hkv || ps != sa.plan_seg_off || gw_lo < 0 || gw_hi >= sa.tw) return;
   } else {
     L = a.lens[b];
     L = L < cap ? L : cap;
@@ -977,6 +987,7 @@ struct PlanArgs {
   int32_t* plan;
   int batch, hkv, bs, log2_bs, cap, tw, min_tiles;
   int seg_off, tile_off;  // word offsets of the segment records and tile descriptors
+  int wave_cap;           // descriptor slots per wavefront
 };
 
 __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArgs p) {
@@ -1021,6 +1032,8 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArg
     p.plan[3] = p.hkv;
     p.plan[kPlanTileOffWord] = p.tile_off;
     p.plan[kPlanSegOffWord] = p.seg_off;
+    p.plan[kPlanWaveCapWord] = p.wave_cap;
+    p.plan[7] = 0;
   }
   // Wavefront ranges: the same split as the in-kernel path.
   for (int g = gtid; g < W; g += gstride) {
@@ -1047,9 +1060,12 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArg
     r[2] = lo_split;
     r[3] = L;
   }
-  // Tile descriptors: tile x of the global sequence (sequence-major, then kv head, then key tile).
+  // Tile descriptors: tile x of the global sequence (sequence-major, then kv head, then key
+  // tile), in slot x - lo of its wavefront g (the largest g with g * T / W <= x).
   uint2* td = reinterpret_cast<uint2*>(p.plan + p.tile_off);
   for (int64_t x = gtid; x < T; x += gstride) {
+    const int64_t g = ((x + 1) * W - 1) / T;
+    const int64_t slot = g * p.wave_cap + (x - g * T / W);
     int lb = 0, ub = B - 1;  // largest b with Hkv * P[b] <= x; its segment is not empty
     while (lb < ub) {
       const int mid = (lb + ub + 1) >> 1;
@@ -1066,7 +1082,7 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArg
     const uint32_t meta = static_cast<uint32_t>(b) | (static_cast<uint32_t>(kvh) << 16) |
                           (static_cast<uint32_t>(nvalid) << 24) | (t == 0 ? 1u << 29 : 0u) |
                           (t == n - 1 ? 1u << 30 : 0u);
-    td[x] = make_uint2(row0, meta);
+    td[slot] = make_uint2(row0, meta);
   }
 }
 
@@ -1152,15 +1168,21 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, i
 
 namespace {
 struct PlanLayout {
-  int64_t seg_off, tile_off, words;
+  int64_t seg_off, tile_off, wave_cap, words;
 };
 PlanLayout plan_layout(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks) {
   PlanLayout l{};
   const int64_t tiles_per_seq = (static_cast<int64_t>(max_blocks) * block_size + 15) / 16;
+  const int64_t max_tiles = static_cast<int64_t>(batch) * num_kv_heads * tiles_per_seq;
+  // A wavefront's range holds at most ceil(T / W) tiles: ceil(max_tiles / tw) when all tw
+  // wavefronts are active, else (W = ceil(T / min_tiles)) at most min_tiles.
+  const int64_t min_tiles = stream_min_tiles();
+  const int64_t per_wave = (max_tiles + cfg.tw - 1) / cfg.tw;
+  l.wave_cap = per_wave > min_tiles ? per_wave : min_tiles;
   l.seg_off = kPlanHeader + static_cast<int64_t>(cfg.tw) * kPlanWave;
   l.tile_off = l.seg_off + static_cast<int64_t>(batch) * num_kv_heads * kPlanSeg;
   l.tile_off += l.tile_off & 1;  // descriptors are 8-byte pairs
-  l.words = l.tile_off + 2 * static_cast<int64_t>(batch) * num_kv_heads * tiles_per_seq;
+  l.words = l.tile_off + 2 * (static_cast<int64_t>(cfg.tw) * l.wave_cap + kWave);
   return l;
 }
 }  // namespace
@@ -1170,15 +1192,16 @@ int64_t stream_plan_bytes(const StreamConfig& cfg, int batch, int num_kv_heads, 
   // descriptor's meta word holds the sequence and kv head in 16 and 8 bits.
   if (block_size < 16 || batch > 65535 || num_kv_heads > 255) return 0;
   const PlanLayout l = plan_layout(cfg, batch, num_kv_heads, block_size, max_blocks);
-  if (l.words >= (int64_t{1} << 31)) return 0;
+  if (l.words >= (int64_t{1} << 31) || l.wave_cap >= (int64_t{1} << 30) / cfg.tw) return 0;
   return l.words * 4;
 }
 
 void stream_plan_offsets(const StreamConfig& cfg, int batch, int num_kv_heads, int block_size, int max_blocks,
-                         int32_t* seg_off, int32_t* tile_off) {
+                         int32_t* seg_off, int32_t* tile_off, int32_t* wave_cap) {
   const PlanLayout l = plan_layout(cfg, batch, num_kv_heads, block_size, max_blocks);
   *seg_off = static_cast<int32_t>(l.seg_off);
   *tile_off = static_cast<int32_t>(l.tile_off);
+  *wave_cap = static_cast<int32_t>(l.wave_cap);
 }
 
 int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32_t* block_tables, int64_t bt_stride,
@@ -1199,6 +1222,7 @@ int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32
   p.min_tiles = stream_min_tiles();
   p.seg_off = static_cast<int>(l.seg_off);
   p.tile_off = static_cast<int>(l.tile_off);
+  p.wave_cap = static_cast<int>(l.wave_cap);
   // Enough workgroups for about eight descriptors per thread at the largest tile count.
   const int64_t max_tiles = (l.words - l.tile_off) / 2;
   int64_t grid = (max_tiles + 8 * kPlanThreads - 1) / (8 * kPlanThreads);

@@ -47,13 +47,13 @@ _SIGNATURES = {
     "mip_paged_decode": (
         _c.c_int,
         [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
-         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp, _sz, _i32, _vp],
     ),
     "mip_paged_decode_append": (
         _c.c_int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _vp,
          _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
-         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp, _sz, _i32, _vp],
     ),
     "mip_paged_decode_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "mip_paged_decode_plan_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),

@@ -237,9 +237,10 @@ def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
         if plan.dtype != torch.int32 or not plan.is_contiguous():
             raise ValueError("plan must be a contiguous int32 tensor from decode_plan")
     plan_ptr = plan.data_ptr() if plan is not None else None
+    plan_bytes = plan.numel() * 4 if plan is not None else 0
     args = (out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1),
             k_cache.data_ptr(), v_cache.data_ptr(), nb, block_tables.data_ptr(), block_tables.stride(0),
-            context_lens.data_ptr(), b, hq, hkv, d, bs, mb, scale, ws_ptr, ws_bytes, plan_ptr, code,
+            context_lens.data_ptr(), b, hq, hkv, d, bs, mb, scale, ws_ptr, ws_bytes, plan_ptr, plan_bytes, code,
             _stream_ptr(q.device))
     keep = (out, q, k_cache, v_cache, block_tables, context_lens, workspace, plan)
     if append is None:

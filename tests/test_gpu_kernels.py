@@ -286,9 +286,9 @@ def test_fused_append_decode_equals_two_calls(gpu, dtype, d, hq, hkv, bs, algo):
 
 
 def _plan_restated(plan: np.ndarray, lens, tables, hkv, bs, cap):
-    """Host restatement of the work plan from its header (T, W, offsets): wavefront ranges,
-    segment descriptors for the merge and one descriptor per tile (pool row, sequence, kv
-    head, valid keys, segment edges), in the kernel's tile order."""
+    """Host restatement of the work plan from its header (T, W, offsets, slots per wavefront):
+    wavefront ranges, segment descriptors for the merge and one descriptor per tile (pool row,
+    sequence, kv head, valid keys, segment edges) in its wavefront's slots, in tile order."""
     u = plan.view(np.uint32)
     L = [min(max(n, 0), cap) for n in lens]
     tiles = [(n + 15) // 16 for n in L]
@@ -296,11 +296,13 @@ def _plan_restated(plan: np.ndarray, lens, tables, hkv, bs, cap):
     T, W = int(plan[0]), int(plan[1])
     assert T == hkv * pre[-1] and plan[2] == len(lens) and plan[3] == hkv
     assert (T == 0) == (W == 0) and W <= T
-    tile_off, seg_off = int(plan[4]), int(plan[5])
+    tile_off, seg_off, cap = int(plan[4]), int(plan[5]), int(plan[6])
     assert tile_off % 2 == 0 and seg_off >= 8 + 2 * W and tile_off >= seg_off + 4 * len(lens) * hkv
-    assert plan.shape[0] >= tile_off + 2 * T
+    tw = (seg_off - 8) // 2  # wavefront records reserved: one per wavefront of the grid
+    assert plan.shape[0] >= tile_off + 2 * (tw * cap + 64) and W <= tw
     for g in range(W):
         assert list(plan[8 + 2 * g: 10 + 2 * g]) == [g * T // W, (g + 1) * T // W], g
+        assert (g + 1) * T // W - g * T // W <= cap, g
     for b in range(len(lens)):
         for kvh in range(hkv):
             r = plan[seg_off + 4 * (b * hkv + kvh): seg_off + 4 * (b * hkv + kvh) + 4]
@@ -313,10 +315,13 @@ def _plan_restated(plan: np.ndarray, lens, tables, hkv, bs, cap):
             assert list(r) == [g_lo, g_hi - g_lo + 1, int(g_lo * T // W < s0), L[b]]
             for t in range(tiles[b]):
                 x = s0 + t
+                g = ((x + 1) * W - 1) // T  # the wavefront whose range holds tile x
+                assert g * T // W <= x < (g + 1) * T // W
+                slot = g * cap + x - g * T // W
                 blk = tables[b][16 * t // bs]
                 row0 = (blk * hkv + kvh) * bs + (16 * t) % bs
                 meta = b | kvh << 16 | min(16, L[b] - 16 * t) << 24 | int(t == 0) << 29 | int(t == tiles[b] - 1) << 30
-                assert [int(u[tile_off + 2 * x]), int(u[tile_off + 2 * x + 1])] == [row0, meta], (b, kvh, t)
+                assert [int(u[tile_off + 2 * slot]), int(u[tile_off + 2 * slot + 1])] == [row0, meta], (b, kvh, t)
 
 
 @pytest.mark.parametrize("dtype,d,hq,hkv,bs", [("bfloat16", 64, 14, 2, 16), ("float16", 128, 28, 4, 32),

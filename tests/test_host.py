@@ -261,7 +261,7 @@ def test_abi_host_checks_return_before_launch(lib):
     assert app(*null) == E                              # tokens but null pointers
     dec = lib.mip_paged_decode
     dargs = [None, 896, 64, None, 896, 64, None, None, 64, None, 8, None, 0, 14, 2, 64, 16, 8, 0.125, None, 0,
-             None, _native.MIP_BF16, None]
+             None, 0, _native.MIP_BF16, None]
     assert dec(*dargs) == OK                            # batch 0
     g = list(dargs); g[12], g[14] = 4, 3
     assert dec(*g) == E                                 # 14 heads do not split over 3 kv heads
@@ -275,7 +275,7 @@ def test_abi_host_checks_return_before_launch(lib):
     assert fused(*(app + dargs)) == OK                  # batch 0
     nul = list(dargs); nul[12] = 4
     assert fused(*(app + nul)) == E                     # new rows missing
-    bad = list(dargs); bad[22] = 9
+    bad = list(dargs); bad[23] = 9
     assert fused(*(app + bad)) == E                     # unknown dtype
     plan = lib.mip_paged_decode_plan
     assert plan(None, None, 8, 4, 14, 2, 64, 16, 8, _native.MIP_BF16, None, 0, None) == E  # no buffers
