@@ -96,6 +96,7 @@ struct StreamArgs {
   int group;
   int tw;          // wavefronts in the grid
   int min_tiles;   // fewest tiles an active wavefront takes
+  int max_pieces;  // most wavefronts per segment, on average (caps W at segments * max_pieces)
   AppendRows app;
   const int32_t* plan;  // stream work plan for these context lengths (nullptr: derive it in-kernel)
   // 32-bit copies of the 64-bit strides / sizes of DecodeArgs (the host checks they fit), so
@@ -149,9 +150,15 @@ __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
   return x;
 }
 
-__device__ __forceinline__ int stream_active_waves(int tw, int total_tiles, int min_tiles) {
+// Active wavefronts W of the stream split: at most the grid's tw, at least min_tiles tiles
+// each, and at most max_pieces per segment on average, so that a few long sequences are not
+// cut into hundreds of pieces each (the merge combines a segment's pieces serially).
+__device__ __forceinline__ int stream_active_waves(int tw, int total_tiles, int min_tiles, int64_t segments,
+                                                   int max_pieces) {
   const int want = (total_tiles + min_tiles - 1) / min_tiles;
-  const int w = want < tw ? want : tw;
+  int w = want < tw ? want : tw;
+  const int64_t cap = segments * max_pieces;
+  if (cap < w) w = static_cast<int>(cap);
   return w > 0 ? w : 1;
 }
 

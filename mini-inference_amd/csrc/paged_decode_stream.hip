@@ -56,6 +56,9 @@ namespace {
 #ifndef MIP_STREAM_PRIO
 #define MIP_STREAM_PRIO 1
 #endif
+#ifndef MIP_STREAM_MAX_PIECES
+#define MIP_STREAM_MAX_PIECES 64
+#endif
 constexpr int kSW = MIP_STREAM_WAVES;   // wavefronts per workgroup
 constexpr int kStreamMaxBatch = 4096;   // context lengths + tile prefix fit in LDS
 
@@ -207,7 +210,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
   if (blockIdx.x == 0) {
     for (int i = tid; i <= B; i += kSW * kWave) sa.ws_prefix[i] = s_pre[i];
   }
-  const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
+  const int tw = stream_active_waves(sa.tw, total, sa.min_tiles, static_cast<int64_t>(sa.batch) * a.hkv, sa.max_pieces);
   const bool active = total > 0 && gw < tw;
   if (active) {
     lo = static_cast<int>(static_cast<int64_t>(gw) * total / tw);
@@ -874,7 +877,7 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
   }
   if constexpr (!PLANNED) {
     const int total = a.hkv * sa.ws_prefix[sa.batch];
-    const int tw = stream_active_waves(sa.tw, total, sa.min_tiles);
+    const int tw = stream_active_waves(sa.tw, total, sa.min_tiles, static_cast<int64_t>(sa.batch) * a.hkv, sa.max_pieces);
     const int n = (L + 15) >> 4;
     const int64_t s0 = static_cast<int64_t>(a.hkv) * sa.ws_prefix[b] + static_cast<int64_t>(kvh) * n;
     const int64_t e1 = s0 + n - 1;
@@ -985,7 +988,7 @@ struct PlanArgs {
   const int32_t* bt;
   int64_t bt_stride;
   int32_t* plan;
-  int batch, hkv, bs, log2_bs, cap, tw, min_tiles;
+  int batch, hkv, bs, log2_bs, cap, tw, min_tiles, max_pieces;
   int seg_off, tile_off;  // word offsets of the segment records and tile descriptors
   int wave_cap;           // descriptor slots per wavefront
 };
@@ -1023,7 +1026,9 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArg
   }
   __syncthreads();
   const int64_t T = static_cast<int64_t>(p.hkv) * s_pre[B];
-  const int W = T > 0 ? stream_active_waves(p.tw, static_cast<int>(T), p.min_tiles) : 0;
+  const int W = T > 0 ? stream_active_waves(p.tw, static_cast<int>(T), p.min_tiles,
+                                            static_cast<int64_t>(B) * p.hkv, p.max_pieces)
+                     : 0;
   const int gtid = blockIdx.x * kPlanThreads + tid, gstride = gridDim.x * kPlanThreads;
   if (gtid == 0) {
     p.plan[0] = static_cast<int32_t>(T);
@@ -1130,6 +1135,17 @@ int stream_min_tiles() {
   return 4;
 }
 
+// Most pieces per segment on average (see stream_active_waves). 64 measured best for one to
+// four long sequences (B=1 at 32k keys: 74 -> 32 us per call; 128: 31 us, 256: 42 us, 32:
+// 46 us) and leaves batches of hundreds of sequences untouched.
+int stream_max_pieces() {
+  if (const char* env = std::getenv("MIP_STREAM_MAX_PIECES")) {
+    const int v = std::atoi(env);
+    if (v > 0) return v;
+  }
+  return MIP_STREAM_MAX_PIECES;
+}
+
 }  // namespace
 
 StreamConfig stream_config(int dtype, int d, int group, int batch) {
@@ -1159,6 +1175,7 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, i
   StreamArgs sa = sa_in;
   sa.tw = cfg.tw;
   sa.min_tiles = stream_min_tiles();
+  sa.max_pieces = stream_max_pieces();
   sa.rec_stride = static_cast<int>(cfg.rec_floats);
   const int fused = sa.app.slots != nullptr, planned = sa.plan != nullptr;
   hipLaunchKernelGGL(p.main[fused][planned], dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
@@ -1175,10 +1192,14 @@ PlanLayout plan_layout(const StreamConfig& cfg, int batch, int num_kv_heads, int
   const int64_t tiles_per_seq = (static_cast<int64_t>(max_blocks) * block_size + 15) / 16;
   const int64_t max_tiles = static_cast<int64_t>(batch) * num_kv_heads * tiles_per_seq;
   // A wavefront's range holds at most ceil(T / W) tiles: ceil(max_tiles / tw) when all tw
-  // wavefronts are active, else (W = ceil(T / min_tiles)) at most min_tiles.
+  // wavefronts are active, at most min_tiles when W = ceil(T / min_tiles), and at most
+  // ceil(max_tiles / (segments * max_pieces)) when the piece cap sets W.
   const int64_t min_tiles = stream_min_tiles();
   const int64_t per_wave = (max_tiles + cfg.tw - 1) / cfg.tw;
+  const int64_t seg_cap = static_cast<int64_t>(batch) * num_kv_heads * stream_max_pieces();
+  const int64_t per_piece = (max_tiles + seg_cap - 1) / seg_cap;
   l.wave_cap = per_wave > min_tiles ? per_wave : min_tiles;
+  if (per_piece > l.wave_cap) l.wave_cap = per_piece;
   l.seg_off = kPlanHeader + static_cast<int64_t>(cfg.tw) * kPlanWave;
   l.tile_off = l.seg_off + static_cast<int64_t>(batch) * num_kv_heads * kPlanSeg;
   l.tile_off += l.tile_off & 1;  // descriptors are 8-byte pairs
@@ -1220,6 +1241,7 @@ int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32
   p.cap = max_blocks * block_size;
   p.tw = cfg.tw;
   p.min_tiles = stream_min_tiles();
+  p.max_pieces = stream_max_pieces();
   p.seg_off = static_cast<int>(l.seg_off);
   p.tile_off = static_cast<int>(l.tile_off);
   p.wave_cap = static_cast<int>(l.wave_cap);
