@@ -22,7 +22,11 @@
 // and then, over all 32 keys,
 //   O^T[D x 16 rows]      += V^T . P^T    v_mfma_f32_16x16x32, D/16 tiles (bf16: P split hi + lo)
 // with a base-2 online softmax per row, as in the decode kernels. Rows whose position is below
-// a key mask it out; a wavefront skips tiles that lie beyond all of its rows' positions.
+// a key mask it out; a wavefront skips tiles that lie beyond all of its rows' positions, and a
+// column block skips the masking in steps whose keys all of its live rows see (most of them).
+// The kernel is VALU-bound, so the softmax step is kept short: the rescale test on each lane's
+// maximum, the scale folded into the exponent's fma, and (fp16) the row sums taken from the
+// packed fp16 weights with v_dot2.
 #include "paged_decode_common.h"
 
 namespace mip {
@@ -144,6 +148,16 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
       qreg[c][kc] = live[c] ? *reinterpret_cast<const uint4*>(qrow + (32 * kc + 8 * grp) * 2) : make_uint4(0, 0, 0, 0);
   }
   wave_pmax = __builtin_amdgcn_readfirstlane(wave_pmax < cap - 1 ? wave_pmax : cap - 1);
+  // Per column block, the smallest position of its live rows (a key at or below it is
+  // visible to every live row of the block).
+  int pmin[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    int v = live[c] ? pos[c] : 0x7fffffff;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) v = min(v, __shfl_xor(v, d));
+    pmin[c] = __builtin_amdgcn_readfirstlane(v);
+  }
 
   // ---- loader: this thread's K / V chunks of a tile. The block ids of a tile are read one
   // tile ahead of its rows, so the table lookup does not add a second latency per tile.
@@ -242,12 +256,15 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
       }
       bool kok[8];
       int kidx[8];
+      bool allok = true;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int r = (i < 4 ? 0 : 12) + 4 * grp + i;
         kok[i] = s_ok[stage][32 * h + r] != 0;
         kidx[i] = key0 + r;
+        allok = allok && kok[i];
       }
+      allok = __all(allok);  // every key of this 32-key step lies in a valid block
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         f32x4_t s0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
@@ -256,18 +273,19 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
           s0 = Ops::qk(kreg[0][kc], qreg[c][kc], s0);
           s1 = Ops::qk(kreg[1][kc], qreg[c][kc], s1);
         }
+        // Raw scores; masked ones become -inf, which only steps with a key past some row's
+        // position or in an invalid block need (a wave-uniform test).
         float sv[8];
-        bool need = false;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float raw = i < 4 ? s0[i] : s1[i - 4];
-          sv[i] = (kok[i] && kidx[i] <= pos[c]) ? raw * a.scale_log2 : -INFINITY;
-          need |= sv[i] > m[c] + kRescaleLog2;
+        for (int i = 0; i < 8; ++i) sv[i] = i < 4 ? s0[i] : s1[i - 4];
+        if (!(allok && key0 + 31 <= pmin[c])) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) sv[i] = (kok[i] && kidx[i] <= pos[c]) ? sv[i] : -INFINITY;
         }
-        if (__any(need)) {
-          float mx = sv[0];
-#pragma unroll
-          for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+        // The rescale test on the lane's maximum, scaled once (the scale is positive).
+        const float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                               fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]))) * a.scale_log2;
+        if (__any(mx > m[c] + kRescaleLog2)) {
           const float mn = fmaxf(m[c], max4(mx));
           const float alpha = (m[c] == -INFINITY) ? 0.0f : fast_exp2(m[c] - mn);
           l[c] *= alpha;
@@ -275,17 +293,28 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
           for (int mt = 0; mt < MT; ++mt) acc[c][mt] *= alpha;
           m[c] = mn;
         }
+        // exp2(-inf - m) = 0 for any finite m; m is -inf only while every score of the row
+        // so far is -inf, and then exp2(-inf - 0) = 0 as well.
+        const float msafe = m[c] == -INFINITY ? 0.0f : m[c];
         float pr[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pr[i] = sv[i] == -INFINITY ? 0.0f : fast_exp2(sv[i] - m[c]);
-          l[c] += pr[i];
-        }
+        for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(fmaf(sv[i], a.scale_log2, -msafe));
         uint4 ph;
         ph.x = Ops::pack2(pr[0], pr[1]);
         ph.y = Ops::pack2(pr[2], pr[3]);
         ph.z = Ops::pack2(pr[4], pr[5]);
         ph.w = Ops::pack2(pr[6], pr[7]);
+        if constexpr (kSplitP<DT>) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) l[c] += pr[i];
+        } else {
+          // Row sum of the fp16 weights the PV product uses: packed pairs against (1, 1).
+          constexpr uint32_t kOnes = 0x3c003c00u;
+          l[c] = dot2<DT>(ph.x, kOnes, l[c]);
+          l[c] = dot2<DT>(ph.y, kOnes, l[c]);
+          l[c] = dot2<DT>(ph.z, kOnes, l[c]);
+          l[c] = dot2<DT>(ph.w, kOnes, l[c]);
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[c][mt] = Ops::qk(vt[mt], ph, acc[c][mt]);
         if constexpr (kSplitP<DT>) {
