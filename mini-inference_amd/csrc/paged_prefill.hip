@@ -26,7 +26,7 @@
 // column block skips the masking in steps whose keys all of its live rows see (most of them).
 // The kernel is VALU-bound, so the softmax step is kept short: the rescale test on each lane's
 // maximum, the scale folded into the exponent's fma, and (fp16) the row sums taken from the
-// packed fp16 weights with v_dot2.
+// packed fp16 weights with v_dot2; V^T comes from transposing LDS reads.
 #include "paged_decode_common.h"
 
 namespace mip {
@@ -83,6 +83,16 @@ __device__ __forceinline__ float max4(float x) {
 // the 2e-3 bound on outputs that are convex combinations of the values; bf16 (2^-8) is split
 // into a rounded part and its remainder, each multiplied by V^T.
 template <int DT> constexpr bool kSplitP = DT == MIP_BF16;
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane j supplies 4 consecutive 16-bit
+// elements A[j][0..3]; lane i receives A[i / 4][i % 4], A[4 + i / 4][i % 4],
+// A[8 + i / 4][i % 4], A[12 + i / 4][i % 4] (as measured on gfx950).
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_tr16(const char* p) {
+  typedef __attribute__((address_space(3))) v4i16_t lv4_t;
+  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lv4_t*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
 
 template <int D>
 struct PShape {
@@ -243,16 +253,16 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
       // The PV product runs over all 32 keys at once (16x16x32). Its k index 8 grp + i stands
       // for key 4 grp + i (i < 4) or 16 + 4 grp + i - 4: exactly the keys this lane's two S^T
       // halves hold, so P needs no lane exchange; V^T is read in the same key order.
+      // Transposing LDS reads (ds_read_b64_tr_b16): in each 16-lane group, lane j = 4k + r
+      // points at dims 16 mt + 4r .. +3 of key 4 grp + k, and lane i16 receives dim
+      // 16 mt + i16 of keys 4 grp + 0..3 (then the same 16 keys later).
       uint4 vt[MT];
-      const uint16_t* v0 = reinterpret_cast<const uint16_t*>(st + P::TILE + (4 * grp) * RB) + i16;
-      const uint16_t* v1 = v0 + 16 * D;
+      const char* vb = st + P::TILE + (4 * grp + (i16 >> 2)) * RB + (i16 & 3) * 8;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int o = 16 * mt;
-        vt[mt].x = static_cast<uint32_t>(v0[o]) | (static_cast<uint32_t>(v0[D + o]) << 16);
-        vt[mt].y = static_cast<uint32_t>(v0[2 * D + o]) | (static_cast<uint32_t>(v0[3 * D + o]) << 16);
-        vt[mt].z = static_cast<uint32_t>(v1[o]) | (static_cast<uint32_t>(v1[D + o]) << 16);
-        vt[mt].w = static_cast<uint32_t>(v1[2 * D + o]) | (static_cast<uint32_t>(v1[3 * D + o]) << 16);
+        const uint2 lo = lds_tr16(vb + 32 * mt);
+        const uint2 hi = lds_tr16(vb + 16 * RB + 32 * mt);
+        vt[mt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
       bool kok[8];
       int kidx[8];
