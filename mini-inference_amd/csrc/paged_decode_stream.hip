@@ -25,9 +25,8 @@
 //     tables and context lengths are read with scalar loads, and cross-lane sums use
 //     v_permlane{16,32}_swap, so nothing else in the loop touches LDS.
 //   * K and q rows are stored with their 16-byte chunks XOR-swizzled by row, so the 16 rows
-//     read by one ds_read_b128 hit distinct banks. V is stored plainly; its transposed reads
-//     (ds_read_u16, one key per read, packed in pairs after the wait) have at most 4-way
-//     conflicts.
+//     read by one ds_read_b128 hit distinct banks. V is stored plainly and read with gfx950's
+//     transposing ds_read_b64_tr_b16 (4 keys of one dim per lane, one read per 16 dims).
 //
 // Tile arithmetic (lane l: row/head l%16, lane group l/16):
 //   S^T[16 keys x 16 heads] = K . Q^T        v_mfma_f32_16x16x32_{bf16,f16}, D/32 steps
@@ -101,13 +100,14 @@ __device__ __forceinline__ u32x4_t lds_b128(uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
   return r;
 }
-// Zero-extending 16-bit read into its own register. (The d16 / d16_hi forms that fill half a
-// register keep the other half as it was when the read was issued, so two of them in flight
-// to one register lose the first; the halves are packed after the wait instead.)
+// Transposing read (ds_read_b64_tr_b16): within each 16-lane group, lane j supplies the
+// address of 4 consecutive 16-bit elements A[j][0..3], and lane i receives A[i / 4][i % 4],
+// A[4 + i / 4][i % 4], A[8 + i / 4][i % 4], A[12 + i / 4][i % 4] (layout measured on gfx950).
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 template <int OFF>
-__device__ __forceinline__ uint32_t lds_u16(uint32_t addr) {
-  uint32_t r;
-  asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+__device__ __forceinline__ u32x2_t lds_tr16(uint32_t addr) {
+  u32x2_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
   return r;
 }
 // Wait for the asm LDS reads, then pass each destination through an empty asm so every use
@@ -115,6 +115,7 @@ __device__ __forceinline__ uint32_t lds_u16(uint32_t addr) {
 __device__ __forceinline__ void lgkm_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ void after_wait(u32x4_t& r) { asm volatile("" : "+v"(r)); }
 __device__ __forceinline__ void after_wait(uint32_t& r) { asm volatile("" : "+v"(r)); }
+__device__ __forceinline__ void after_wait(u32x2_t& r) { asm volatile("" : "+v"(r)); }
 
 // Sum / max over the four lanes l, l^16, l^32, l^48 with VALU lane swaps.
 __device__ __forceinline__ float sum4(float x) {
@@ -258,7 +259,9 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     k_addr[kc] = ring + R::K_OFF + i16 * RB + ((c ^ (i16 & (CPR - 1))) * 16);
     q_addr[kc] = ring + R::Q_OFF + qrow * RB + ((c ^ (qrow & (CPR - 1))) * 16);
   }
-  const uint32_t v_addr = ring + R::V_OFF + (4 * grp) * RB + i16 * 2;
+  // V^T operand by transposing reads: lane i16 = 4k + r points at dims 4r .. 4r + 3 (+16 mt) of
+  // key 4 grp + k and receives dim 16 mt + i16 of keys 4 grp + 0..3.
+  const uint32_t v_addr = ring + R::V_OFF + (4 * grp + (i16 >> 2)) * RB + (i16 & 3) * 8;
   const int dma_r = lane / CPR, dma_pc = lane % CPR;
 
   uint32_t vmask[NS];  // per stage: bit r = key row r of the tile is a key of its segment
@@ -361,14 +364,11 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     u32x4_t kreg[KC];
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) kreg[kc] = lds_b128<SO>(k_addr[kc]);
-    uint32_t ve[MT][4];  // V^T operand halves: keys 4*grp + e at dim 16*mt + i16
+    u32x2_t ve[MT];  // V^T operand: keys 4*grp + 0..3 at dim 16*mt + i16, packed in pairs
     if (vm) {
       static_for<0, MT>([&](auto mtc) {
         constexpr int mt = decltype(mtc)::value;
-        ve[mt][0] = lds_u16<SO + 0 * RB + 32 * mt>(v_addr);
-        ve[mt][1] = lds_u16<SO + 1 * RB + 32 * mt>(v_addr);
-        ve[mt][2] = lds_u16<SO + 2 * RB + 32 * mt>(v_addr);
-        ve[mt][3] = lds_u16<SO + 3 * RB + 32 * mt>(v_addr);
+        ve[mt] = lds_tr16<SO + 32 * mt>(v_addr);
       });
     }
     lgkm_wait();
@@ -378,10 +378,9 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     if (vm) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) after_wait(ve[mt][e]);
-        vt[mt][0] = ve[mt][0] | (ve[mt][1] << 16);
-        vt[mt][1] = ve[mt][2] | (ve[mt][3] << 16);
+        after_wait(ve[mt]);
+        vt[mt][0] = ve[mt][0];
+        vt[mt][1] = ve[mt][1];
       }
     }
 
@@ -571,7 +570,9 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
     k_addr[kc] = ring + R::K_OFF + i16 * RB + ((c ^ (i16 & (CPR - 1))) * 16);
     q_addr[kc] = ring + R::Q_OFF + qrow * RB + ((c ^ (qrow & (CPR - 1))) * 16);
   }
-  const uint32_t v_addr = ring + R::V_OFF + (4 * grp) * RB + i16 * 2;
+  // V^T operand by transposing reads: lane i16 = 4k + r points at dims 4r .. 4r + 3 (+16 mt) of
+  // key 4 grp + k and receives dim 16 mt + i16 of keys 4 grp + 0..3.
+  const uint32_t v_addr = ring + R::V_OFF + (4 * grp + (i16 >> 2)) * RB + (i16 & 3) * 8;
   const int dma_r = lane / CPR, dma_pc = lane % CPR;
   // Lane offsets inside a tile's rows (row r < valid keys; other rows re-read row 0).
   uint32_t k_lane[R::KI], v_lane[R::KI];
@@ -693,14 +694,11 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
     u32x4_t kreg[KC];
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) kreg[kc] = lds_b128<SO>(k_addr[kc]);
-    uint32_t ve[MT][4];  // V^T operand halves: keys 4*grp + e at dim 16*mt + i16
+    u32x2_t ve[MT];  // V^T operand: keys 4*grp + 0..3 at dim 16*mt + i16, packed in pairs
     if (vm) {
       static_for<0, MT>([&](auto mtc) {
         constexpr int mt = decltype(mtc)::value;
-        ve[mt][0] = lds_u16<SO + 0 * RB + 32 * mt>(v_addr);
-        ve[mt][1] = lds_u16<SO + 1 * RB + 32 * mt>(v_addr);
-        ve[mt][2] = lds_u16<SO + 2 * RB + 32 * mt>(v_addr);
-        ve[mt][3] = lds_u16<SO + 3 * RB + 32 * mt>(v_addr);
+        ve[mt] = lds_tr16<SO + 32 * mt>(v_addr);
       });
     }
     lgkm_wait();
@@ -710,10 +708,9 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
     if (vm) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) after_wait(ve[mt][e]);
-        vt[mt][0] = ve[mt][0] | (ve[mt][1] << 16);
-        vt[mt][1] = ve[mt][2] | (ve[mt][3] << 16);
+        after_wait(ve[mt]);
+        vt[mt][0] = ve[mt][0];
+        vt[mt][1] = ve[mt][1];
       }
     }
 
