@@ -50,7 +50,7 @@ namespace {
 #define MIP_STREAM_STAGES_D64 3
 #endif
 #ifndef MIP_STREAM_STAGES_D128
-#define MIP_STREAM_STAGES_D128 2
+#define MIP_STREAM_STAGES_D128 3
 #endif
 #ifndef MIP_STREAM_PRIO
 #define MIP_STREAM_PRIO 1
