@@ -9,11 +9,11 @@
 // only each sequence's own causal range is computed. With ctx_start = 0 this is the packed
 // block-diagonal causal prefill of engine/kv_cache.py:290-294.
 //
-// Work split: workgroup (kv head, sequence, block of TQ new tokens), 4 wavefronts. The query
-// rows of a workgroup are (token, head of the kv head's group) pairs: a 16-row column block
-// holds 16 / QR tokens x QR head slots (the group's G heads, padded to QR), and each
-// wavefront owns NC column blocks. Blocks of the same sequence are dispatched latest-first,
-// since later tokens see more keys.
+// Work split: an item is (kv head, sequence, block of TQ new tokens), done by a workgroup of
+// 4 wavefronts. The query rows of an item are (token, head of the kv head's group) pairs: a
+// 16-row column block holds 16 / QR tokens x QR head slots (the group's G heads, padded to
+// QR), and each wavefront owns NC column blocks. The grid is persistent and walks a
+// longest-first work list (paged_prefill_kernel).
 //
 // Per 32-key tile: all 256 threads copy the K and V rows (found through the block table) into
 // an LDS stage (two stages: the next tile's rows are fetched into registers while the current
@@ -63,6 +63,7 @@ struct PrefillArgs {
   const int32_t* cu_q;       // [S + 1] packed row offsets of each sequence's new tokens
   const int32_t* ctx_start;  // [S] tokens cached before this pass (position of token 0)
   int hkv, group, bs, log2_bs, max_blocks;
+  int num_seqs, zb;        // sequences; blocks of TQ new tokens the longest one can have
   float scale_log2;
 };
 
@@ -106,19 +107,18 @@ struct PShape {
   static_assert(NLD >= 1 && NLD * kPW * kWave == kKT * CPR, "tile must split evenly over the workgroup");
 };
 
+// One work item: new tokens [blk * TQ, blk * TQ + TQ) of sequence s against kv head kvh.
+// smem holds the two K | V stages, s_ok[stage][key] whether a key row is a real key (valid
+// block id). Called by the whole workgroup (the barriers inside are workgroup-wide).
 template <int DT, int D, int QR, int NC>
-__global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs a) {
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int s, int blk, char* smem,
+                                             uint8_t (*s_ok)[kKT]) {
   using P = PShape<D>;
   using Ops = MfmaOps<DT>;
   constexpr int RB = P::RB, CPR = P::CPR, KC = P::KC, MT = P::MT;
   constexpr int TPC = 16 / QR;                 // tokens per column block
   constexpr int TQ = kPW * NC * TPC;           // tokens per workgroup
-  __shared__ __attribute__((aligned(16))) char smem[2 * P::STAGE];
-  __shared__ uint8_t s_ok[2][kKT];             // key row holds a real key (valid block id)
 
-  const int kvh = blockIdx.x;
-  const int s = blockIdx.y;
-  const int blk = gridDim.z - 1 - blockIdx.z;  // latest tokens (most keys) first
   const int q0 = a.cu_q[s];
   const int n_s = a.cu_q[s + 1] - q0;
   const int tok_lo = blk * TQ;
@@ -364,14 +364,131 @@ __global__ __launch_bounds__(kPW * kWave) void paged_prefill_kernel(PrefillArgs 
   }
 }
 
+// Work list of the persistent kernel, built in LDS by every workgroup from cu_q: sequences
+// sorted by their number of TQ-token blocks (descending), and the items ordered by block
+// index, highest first (later tokens see more keys), then by sorted sequence, then kv head,
+// so the longest items start first. Limits: kMaxSeqs sequences, kMaxLevels blocks each.
+constexpr int kMaxSeqs = 1024;
+constexpr int kMaxLevels = kPW * kWave - 1;  // 255: one scan entry per thread
+
+__device__ __forceinline__ int block_inclusive_scan(int x, int* s_wtot) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int incl = decode::wave_inclusive_scan(x, lane);
+  if (lane == kWave - 1) s_wtot[w] = incl;
+  __syncthreads();
+  int off = 0;
+  for (int j = 0; j < w; ++j) off += s_wtot[j];
+  __syncthreads();  // s_wtot is reused by the next scan
+  return incl + off;
+}
+
+// Two wavefronts per SIMD is the occupancy the register file allows at these tile sizes;
+// saying so lets the compiler use up to 256 registers instead of spilling.
+template <int DT, int D, int QR, int NC, bool PERSIST>
+__global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_prefill_kernel(
+    PrefillArgs a) {
+  using P = PShape<D>;
+  constexpr int TQ = kPW * NC * (16 / QR);
+  __shared__ __attribute__((aligned(16))) char smem[2 * P::STAGE];
+  __shared__ uint8_t s_ok[2][kKT];
+  if constexpr (!PERSIST) {
+    // One workgroup per (kv head, sequence, block), blocks of a sequence latest first.
+    prefill_item<DT, D, QR, NC>(a, blockIdx.x, blockIdx.y, gridDim.z - 1 - blockIdx.z, smem, s_ok);
+  } else {
+    __shared__ int s_nb[kMaxSeqs];          // blocks of sequence s
+    __shared__ int s_seq[kMaxSeqs];         // sequences by blocks, descending
+    __shared__ int s_cnt[kMaxLevels + 1];   // histogram, then sequences with more than v blocks
+    __shared__ int s_fill[kMaxLevels + 1];
+    __shared__ int s_ipre[kMaxLevels + 1];  // first item of the k-th level, highest level first
+    __shared__ int s_wtot[kPW];
+    const int tid = threadIdx.x, S = a.num_seqs, zb = a.zb;
+    for (int v = tid; v <= zb; v += kPW * kWave) {
+      s_cnt[v] = 0;
+      s_fill[v] = 0;
+    }
+    __syncthreads();
+    for (int q = tid; q < S; q += kPW * kWave) {
+      const int n = a.cu_q[q + 1] - a.cu_q[q];
+      int nb = n > 0 ? (n + TQ - 1) / TQ : 0;
+      nb = nb < zb ? nb : zb;
+      s_nb[q] = nb;
+      atomicAdd(&s_cnt[nb], 1);
+    }
+    __syncthreads();
+    // Thread t takes bin zb - t: the inclusive scan counts the sequences with at least that many
+    // blocks, i.e. more than zb - t - 1.
+    const int hv = tid <= zb ? s_cnt[zb - tid] : 0;
+    const int ge = block_inclusive_scan(hv, s_wtot);
+    if (tid < zb) s_cnt[zb - tid - 1] = ge;  // sequences with more than zb - tid - 1 blocks
+    if (tid == 0) s_cnt[zb] = 0;
+    __syncthreads();
+    for (int q = tid; q < S; q += kPW * kWave) {
+      const int nb = s_nb[q];
+      s_seq[s_cnt[nb] + atomicAdd(&s_fill[nb], 1)] = q;
+    }
+    // Items of level lv = zb - 1 - k (k-th from the top): one per (sequence with more than lv
+    // blocks, kv head).
+    const int items = tid < zb ? s_cnt[zb - 1 - tid] * a.hkv : 0;
+    const int incl = block_inclusive_scan(items, s_wtot);
+    if (tid < zb) s_ipre[tid + 1] = incl;
+    if (tid == 0) s_ipre[0] = 0;
+    __syncthreads();
+    const int total = s_ipre[zb];
+    // Rounds of gridDim.x items, alternating direction, so a workgroup that drew a long item in
+    // one round draws a short one in the next.
+    const int G = gridDim.x;
+    for (int r = 0; r * G < total; ++r) {
+      const int it = r * G + ((r & 1) ? G - 1 - static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x));
+      if (it >= total) continue;
+      int lo = 0, hi = zb - 1;  // the level k with s_ipre[k] <= it < s_ipre[k + 1]
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_ipre[mid] <= it) lo = mid; else hi = mid - 1;
+      }
+      const int rem = it - s_ipre[lo];
+      const int seq = __builtin_amdgcn_readfirstlane(s_seq[rem / a.hkv]);
+      const int kvh = __builtin_amdgcn_readfirstlane(rem % a.hkv);
+      const int blk = __builtin_amdgcn_readfirstlane(zb - 1 - lo);
+      prefill_item<DT, D, QR, NC>(a, kvh, seq, blk, smem, s_ok);
+    }
+  }
+}
+
 template <int D> constexpr int kNC = MIP_PREFILL_NC > 0 ? MIP_PREFILL_NC : (D == 64 ? 4 : 2);
 
+// Workgroups of the persistent kernel that fit on the device at once (0 on error).
+template <int DT, int D, int QR, int NC>
+int persistent_grid() {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, reinterpret_cast<const void*>(paged_prefill_kernel<DT, D, QR, NC, true>), kPW * kWave, 0) !=
+      hipSuccess)
+    return 0;
+  return cus * (per_cu > 0 ? per_cu : 1);
+}
+
 template <int DT, int D, int QR>
-int launch_shape(const PrefillArgs& a, int num_seqs, int max_q_len, hipStream_t s) {
+int launch_shape(PrefillArgs a, int num_seqs, int max_q_len, hipStream_t s) {
   constexpr int NC = kNC<D>;
   constexpr int TQ = kPW * NC * (16 / QR);
   const int zb = (max_q_len + TQ - 1) / TQ;
-  hipLaunchKernelGGL((paged_prefill_kernel<DT, D, QR, NC>), dim3(a.hkv, num_seqs, zb), dim3(kPW * kWave), 0, s, a);
+  a.num_seqs = num_seqs;
+  a.zb = zb;
+  // Persistent grid over a longest-first work list where it fits in LDS: a grid with one
+  // workgroup per (kv head, sequence, block) leaves most of the device idle when lengths vary,
+  // since the workgroups past a sequence's end occupy the dispatcher.
+  static const int grid_cap = persistent_grid<DT, D, QR, NC>();
+  const int64_t items = static_cast<int64_t>(a.hkv) * num_seqs * zb;
+  if (grid_cap > 0 && num_seqs <= kMaxSeqs && zb <= kMaxLevels) {
+    const int grid = static_cast<int>(items < grid_cap ? items : grid_cap);
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, QR, NC, true>), dim3(grid), dim3(kPW * kWave), 0, s, a);
+  } else {
+    if (num_seqs > 65535 || zb > 65535) return MIP_EUNSUPPORTED;
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, QR, NC, false>), dim3(a.hkv, num_seqs, zb), dim3(kPW * kWave), 0,
+                       s, a);
+  }
   return status_from_hip(hipGetLastError());
 }
 
@@ -404,7 +521,6 @@ extern "C" int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_
   if (!out || !q || !k_cache || !v_cache || !block_tables || !cu_q || !ctx_start) return MIP_EINVAL;
   const int group = num_heads / num_kv_heads;
   if (dtype == MIP_F32 || (head_dim != 64 && head_dim != 128) || group > 16) return MIP_EUNSUPPORTED;
-  if (num_seqs > 65535 || (max_q_len + 3) / 4 > 65535) return MIP_EUNSUPPORTED;
   // q rows are read and output rows written 16 / 8 bytes at a time.
   const uint64_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
                          static_cast<uint64_t>(q_stride_tok * 2) | static_cast<uint64_t>(q_stride_head * 2) |
@@ -416,7 +532,7 @@ extern "C" int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_
   if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return MIP_EINVAL;
   if (num_cache_blocks > INT32_MAX) return MIP_EINVAL;
 
-  prefill::PrefillArgs a;
+  prefill::PrefillArgs a{};
   a.out = static_cast<char*>(out);
   a.out_st = out_stride_tok;
   a.out_sh = out_stride_head;

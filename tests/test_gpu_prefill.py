@@ -197,3 +197,43 @@ def test_prefill_context_kernel_matches_reference_path(gpu, prefix, monkeypatch)
     torch.cuda.synchronize()
     err = (outs[0] - outs[1]).abs().max().item()
     assert err <= 1.6e-2, err  # both sides round to bf16; the reference path also rounds P and its sums
+
+
+def test_paged_prefill_grid_fallbacks(gpu):
+    """The one-workgroup-per-item grid, taken past the persistent kernel's work-list limits:
+    more than 1024 sequences, and one sequence with more than 255 blocks of new tokens (rows
+    of the long one sampled against float64)."""
+    from engine import paged_ops
+
+    announce("paged_prefill 1100 short sequences (per-item grid)")
+    rnd = random.Random(13)
+    lengths = [rnd.randint(1, 3) for _ in range(1100)]
+    starts = [rnd.randint(0, 40) for _ in range(1100)]
+    dev, want = build(gpu, "float16", 64, 14, 2, 16, starts, lengths, seed=13)
+    out = paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], max(lengths))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert float((np.abs(got - want) - half_ulp(want, "float16")).max()) <= 2e-3
+
+    announce("paged_prefill one sequence of 8200 new tokens after 100 cached (per-item grid)")
+    dtype, d, hq, hkv, bs, start, n = "bfloat16", 64, 14, 2, 16, 100, 8200
+    nblk = (start + n + bs - 1) // bs
+    ids = list(range(nblk + 4))
+    rnd.shuffle(ids)
+    table = ids[:nblk]
+    g = torch.Generator(device=gpu).manual_seed(17)
+    k_pool = torch.randn(nblk + 5, hkv, bs, d, generator=g, device=gpu).to(torch.bfloat16)
+    v_pool = torch.randn(nblk + 5, hkv, bs, d, generator=g, device=gpu).to(torch.bfloat16)
+    qkv = torch.randn(n, (hq + 2 * hkv) * d, generator=g, device=gpu).to(torch.bfloat16)
+    q = qkv[:, :hq * d].view(n, hq, d)
+    tab = torch.tensor([table], dtype=torch.int32, device=gpu)
+    cu = torch.tensor([0, n], dtype=torch.int32, device=gpu)
+    out = paged_ops.paged_prefill(q, k_pool, v_pool, tab, cu, torch.tensor([start], dtype=torch.int32, device=gpu), n)
+    torch.cuda.synchronize()
+    kp, vp = k_pool.float().cpu().numpy(), v_pool.float().cpu().numpy()
+    qc, oc = q.float().cpu().numpy(), out.float().cpu().numpy()
+    for r0 in (0, 31, 4000, 8100, n - 33):
+        rows = slice(r0, r0 + 32)
+        want = ref.prefill_attention_f64(qc[rows], kp, vp, [table], [start + r0], [32], bs)
+        err = float((np.abs(oc[rows] - want) - half_ulp(want, dtype)).max())
+        assert err <= 2e-3, (r0, err)
