@@ -224,6 +224,56 @@ def prefill_measure(dev, iters: int = 30) -> dict:
     }
 
 
+def copy_measure(dev, iters: int = 40, sets: int = 8) -> dict:
+    """Copy-on-write of the shared-prefix workload: each of 64 forks copies its partially
+    filled last shared block, every layer, K and V (``mip_copy_blocks``, one launch for all
+    pairs). Pools of 24 layers at the Qwen2.5-0.5B shape (fp16, 2 kv heads, d64, block 16);
+    ``sets`` disjoint sets of 64 (src, dst) pairs are cycled so no launch re-reads what the
+    last one touched. bytes = read + write of 24 * 2 * 2 KiB per pair.
+    """
+    import random
+
+    import torch
+
+    from engine import paged_ops
+
+    layers, hkv, bs, d, pairs_per = 24, 2, 16, 64, 64
+    nb = 2 * sets * pairs_per + 8
+    k = torch.empty(layers, nb + 1, hkv, bs, d, dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    k.normal_(0.0, 1.0, generator=gen)
+    v.normal_(0.0, 1.0, generator=gen)
+    ids = list(range(nb))
+    random.Random(5).shuffle(ids)
+    sets_t = [torch.tensor([[ids[2 * (i * pairs_per + j)], ids[2 * (i * pairs_per + j) + 1]] for j in range(pairs_per)],
+                           dtype=torch.int64, device=dev) for i in range(sets)]
+    it = [0]
+
+    def call():
+        paged_ops.copy_blocks(k, v, sets_t[it[0] % sets])
+        it[0] += 1
+
+    for _ in range(sets):
+        call()
+    torch.cuda.synchronize()
+    t = time_loop(call, iters)
+    nbytes = 2 * pairs_per * layers * 2 * hkv * bs * d * 2
+    gbs = nbytes / t / 1e9
+    return {
+        "workload": f"copy-on-write of {pairs_per} partially filled shared blocks (one per fork), {layers} layers, "
+                    "K and V, fp16, 2 kv heads d64, block 16",
+        "kernel": "copy_blocks_kernel<16>",
+        "us": round(t * 1e6, 2),
+        "bound": "hbm",
+        "achieved": round(gbs, 1),
+        "peak": 8000.0,
+        "unit": "GB/s",
+        "frac": round(gbs / 8000.0, 4),
+        "bytes": nbytes,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -232,7 +282,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (about)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-model", action="store_true", help="skip the full-model decode tok/s measurement")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the packed prefill attention measurement")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the packed prefill attention and block-copy measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 512 MiB device copy three times (HBM counter scale for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -367,6 +418,13 @@ def main() -> int:
         except Exception as exc:
             log(f"prefill measurement failed: {exc!r}")
             result["prefill"] = None
+        try:
+            result["block_copy"] = copy_measure(dev)
+            bc = result["block_copy"]
+            log(f"block copy: {bc['us']} us, {bc['achieved']} GB/s ({bc['frac']:.1%} of peak)")
+        except Exception as exc:
+            log(f"block copy measurement failed: {exc!r}")
+            result["block_copy"] = None
 
     if not args.no_cpu_baseline:
         cb = cpu_baseline(batch, qs[0], ks[0], vs[0], args.cpu_budget)

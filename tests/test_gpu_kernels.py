@@ -136,14 +136,17 @@ def test_append_narrow_rows_and_skipped_slots(gpu, dtype, d):
 # ----------------------------------------------------------------------------- block copy
 
 
-@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
-def test_copy_blocks_bit_exact(gpu, dtype):
+@pytest.mark.parametrize("dtype,hkv,bs,d", [("bfloat16", 2, 16, 64), ("float32", 2, 16, 64),
+                                            ("bfloat16", 4, 32, 128), ("float32", 1, 1, 3)])
+def test_copy_blocks_bit_exact(gpu, dtype, hkv, bs, d):
+    """Whole-block copies, all layers, K and V; a 32 KiB block (4 kv heads x 32 x 128) takes
+    several chunk rounds per thread, a 12-byte block the 4-byte chunk width."""
     from engine import paged_ops
 
-    announce(f"copy_blocks {dtype}")
+    announce(f"copy_blocks {dtype} hkv={hkv} bs={bs} d={d}")
     dt = DTYPES[dtype]
     g = torch.Generator().manual_seed(6)
-    layers, nb, hkv, bs, d = 3, 40, 2, 16, 64
+    layers, nb = 3, 40
     k = torch.randn(layers, nb + 1, hkv, bs, d, generator=g).to(dt).to(gpu)
     v = torch.randn(layers, nb + 1, hkv, bs, d, generator=g).to(dt).to(gpu)
     rng = random.Random(7)
