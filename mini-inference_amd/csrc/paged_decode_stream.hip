@@ -416,12 +416,12 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
         ph[j / 2] = Ops::pack2(p0, p1);
         pl[j / 2] = Ops::pack2(p0 - Ops::lo(ph[j / 2]), p1 - Ops::hi(ph[j / 2]));
       }
+      // One 16x16x32 product per 16 dims: its k index runs over this lane group's 4 keys
+      // twice, V^T repeated against P's rounded part, then against its remainder.
+      const uint4 pb = make_uint4(ph[0], ph[1], pl[0], pl[1]);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint2 va = make_uint2(vt[mt][0], vt[mt][1]);
-        acc[mt] = Ops::pv(va, make_uint2(ph[0], ph[1]), acc[mt]);
-        acc[mt] = Ops::pv(va, make_uint2(pl[0], pl[1]), acc[mt]);
-      }
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = Ops::qk(make_uint4(vt[mt][0], vt[mt][1], vt[mt][0], vt[mt][1]), pb, acc[mt]);
     }
 
     if (ct == cn - 1 || i == hi - 1) {
@@ -745,12 +745,12 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
         ph[j / 2] = Ops::pack2(p0, p1);
         pl[j / 2] = Ops::pack2(p0 - Ops::lo(ph[j / 2]), p1 - Ops::hi(ph[j / 2]));
       }
+      // One 16x16x32 product per 16 dims: its k index runs over this lane group's 4 keys
+      // twice, V^T repeated against P's rounded part, then against its remainder.
+      const uint4 pb = make_uint4(ph[0], ph[1], pl[0], pl[1]);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint2 va = make_uint2(vt[mt][0], vt[mt][1]);
-        acc[mt] = Ops::pv(va, make_uint2(ph[0], ph[1]), acc[mt]);
-        acc[mt] = Ops::pv(va, make_uint2(pl[0], pl[1]), acc[mt]);
-      }
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = Ops::qk(make_uint4(vt[mt][0], vt[mt][1], vt[mt][0], vt[mt][1]), pb, acc[mt]);
     }
 
     if (seg_last || i == hi - 1) {
