@@ -224,6 +224,53 @@ def prefill_measure(dev, iters: int = 30) -> dict:
     }
 
 
+def append_measure(dev, iters: int = 40) -> dict:
+    """Packed prefill append of the shared-prefix workload: every fork's new suffix tokens
+    (U[32, 512] each, 64 forks) scattered into the pool of one layer through the context's
+    slot mapping (``mip_kv_append`` with N tokens), fp16, 2 kv heads d64, block 16. The k/v
+    rows are the model's [1, Hkv, N, D] projections viewed token-major, as the reference
+    scatters them (engine/kv_cache.py:286-289). Four layers are cycled.
+    bytes = read + write of the K and V rows + the int64 slots.
+    """
+    import torch
+
+    from engine import paged_ops, workloads
+
+    pb = workloads.build_prefix_batch(dev, seed=0, num_layers=4)
+    ctx = pb.cache.packed_prefill_context(pb.children, pb.suffix_lens)
+    n = sum(pb.suffix_lens)
+    hkv, d = 2, 64
+    gen = torch.Generator(device=dev).manual_seed(9)
+    ks = [torch.randn(1, hkv, n, d, generator=gen, device=dev).half() for _ in range(4)]
+    vs = [torch.randn(1, hkv, n, d, generator=gen, device=dev).half() for _ in range(4)]
+    calls = [paged_ops.prepare_kv_append(pb.cache.k[i], pb.cache.v[i], ks[i][0].transpose(0, 1),
+                                         vs[i][0].transpose(0, 1), ctx.slot_mapping) for i in range(4)]
+    it = [0]
+
+    def call():
+        calls[it[0] % 4]()
+        it[0] += 1
+
+    for _ in range(4):
+        call()
+    torch.cuda.synchronize()
+    t = time_loop(call, iters)
+    nbytes = 2 * (2 * n * hkv * d * 2) + 8 * n
+    gbs = nbytes / t / 1e9
+    return {
+        "workload": f"packed prefill append: {n} new tokens of {len(pb.children)} forks into one layer's pool, "
+                    "fp16, 2 kv heads d64, block 16",
+        "kernel": "kv_append_kernel",
+        "us_per_layer": round(t * 1e6, 2),
+        "bound": "hbm",
+        "achieved": round(gbs, 1),
+        "peak": 8000.0,
+        "unit": "GB/s",
+        "frac": round(gbs / 8000.0, 4),
+        "bytes": nbytes,
+    }
+
+
 def copy_measure(dev, iters: int = 40, sets: int = 8) -> dict:
     """Copy-on-write of the shared-prefix workload: each of 64 forks copies its partially
     filled last shared block, every layer, K and V (``mip_copy_blocks``, one launch for all
@@ -283,7 +330,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-model", action="store_true", help="skip the full-model decode tok/s measurement")
     ap.add_argument("--no-prefill", action="store_true",
-                    help="skip the packed prefill attention and block-copy measurements")
+                    help="skip the packed prefill attention, packed append and block-copy measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 512 MiB device copy three times (HBM counter scale for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -418,6 +465,13 @@ def main() -> int:
         except Exception as exc:
             log(f"prefill measurement failed: {exc!r}")
             result["prefill"] = None
+        try:
+            result["packed_append"] = append_measure(dev)
+            pa = result["packed_append"]
+            log(f"packed append: {pa['us_per_layer']} us/layer, {pa['achieved']} GB/s ({pa['frac']:.1%} of peak)")
+        except Exception as exc:
+            log(f"packed append measurement failed: {exc!r}")
+            result["packed_append"] = None
         try:
             result["block_copy"] = copy_measure(dev)
             bc = result["block_copy"]
