@@ -30,9 +30,10 @@
 //
 // Tile arithmetic (lane l: row/head l%16, lane group l/16):
 //   S^T[16 keys x 16 heads] = K . Q^T        v_mfma_f32_16x16x32_{bf16,f16}, D/32 steps
-//   O^T[D x 16 heads]      += V^T . P^T      v_mfma_f32_16x16x16_{bf16,f16}, D/16 M-tiles,
+//   O^T[D x 16 heads]      += V^T . P^T      v_mfma_f32_16x16x32_{bf16,f16}, D/16 M-tiles,
 //   P^T is the S^T output layout (kept in registers), split into hi + lo 16-bit parts so the
-//   PV product keeps ~fp32 precision. Online softmax in base 2 with a per-head running max
+//   PV product keeps ~fp32 precision: the 32-deep k index runs over the lane group's 4 keys
+//   twice, V^T against hi and again against lo. Online softmax in base 2 with a per-head running max
 //   that is only raised when a key exceeds it by more than kRescaleLog2.
 #include <cstdlib>
 #include <type_traits>
