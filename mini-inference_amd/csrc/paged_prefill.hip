@@ -73,11 +73,17 @@ __device__ __forceinline__ float sum4(float x) {
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
+// Maxima by IEEE 754-2019 maximum (v_maximum3_f32 on gfx950). fmaxf (maxNum) has to quiet
+// signalling NaNs in IEEE mode, which costs one extra v_max per operand that is not the
+// result of arithmetic (MFMA outputs, lane exchanges); maximum needs no such step. The two
+// differ only on NaN operands, which scores never are.
+__device__ __forceinline__ float fmax2(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float fmax3(float a, float b, float c) { return fmax2(fmax2(a, b), c); }
 __device__ __forceinline__ float max4(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float y = fmax2(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return fmax2(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // P = exp2(s - m) lies in [0, 2^kRescaleLog2]. fp16 holds it to 2^-11 relative, enough for
@@ -215,9 +221,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
 
   f32x4_t acc[NC][MT];
   float m[NC], l[NC];
+  float mth[NC], nm[NC];  // m + kRescaleLog2 (the rescale threshold) and -m (0 while m = -inf)
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     m[c] = -INFINITY;
+    mth[c] = -INFINITY;
+    nm[c] = 0.0f;
     l[c] = 0.0f;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[c][mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -264,14 +273,13 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
         const uint2 hi = lds_tr16(vb + 16 * RB + 32 * mt);
         vt[mt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
+      // The 8 keys of this lane's S^T halves: 4 grp + kr[i].
+      constexpr int kr[8] = {0, 1, 2, 3, 16, 17, 18, 19};
       bool kok[8];
-      int kidx[8];
       bool allok = true;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int r = (i < 4 ? 0 : 12) + 4 * grp + i;
-        kok[i] = s_ok[stage][32 * h + r] != 0;
-        kidx[i] = key0 + r;
+        kok[i] = s_ok[stage][32 * h + 4 * grp + kr[i]] != 0;
         allok = allok && kok[i];
       }
       allok = __all(allok);  // every key of this 32-key step lies in a valid block
@@ -289,26 +297,29 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
 #pragma unroll
         for (int i = 0; i < 8; ++i) sv[i] = i < 4 ? s0[i] : s1[i - 4];
         if (!(allok && key0 + 31 <= pmin[c])) {
+          // Key key0 + kr[i] + 4 grp is visible to this lane's row when kr[i] <= lim.
+          const int lim = pos[c] - key0 - 4 * grp;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) sv[i] = (kok[i] && kidx[i] <= pos[c]) ? sv[i] : -INFINITY;
+          for (int i = 0; i < 8; ++i) sv[i] = (kok[i] && kr[i] <= lim) ? sv[i] : -INFINITY;
         }
         // The rescale test on the lane's maximum, scaled once (the scale is positive).
-        const float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                               fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]))) * a.scale_log2;
-        if (__any(mx > m[c] + kRescaleLog2)) {
-          const float mn = fmaxf(m[c], max4(mx));
+        const float mx = fmax3(fmax3(sv[0], sv[1], sv[2]), fmax3(sv[3], sv[4], sv[5]), fmax2(sv[6], sv[7])) *
+                         a.scale_log2;
+        if (__any(mx > mth[c])) {
+          const float mn = fmax2(m[c], max4(mx));
           const float alpha = (m[c] == -INFINITY) ? 0.0f : fast_exp2(m[c] - mn);
           l[c] *= alpha;
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) acc[c][mt] *= alpha;
           m[c] = mn;
+          mth[c] = mn + kRescaleLog2;
+          // exp2(-inf - m) = 0 for any finite m; m stays -inf only while every score of the
+          // row so far is -inf, and then exp2(-inf - 0) = 0 as well.
+          nm[c] = mn == -INFINITY ? 0.0f : -mn;
         }
-        // exp2(-inf - m) = 0 for any finite m; m is -inf only while every score of the row
-        // so far is -inf, and then exp2(-inf - 0) = 0 as well.
-        const float msafe = m[c] == -INFINITY ? 0.0f : m[c];
         float pr[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(fmaf(sv[i], a.scale_log2, -msafe));
+        for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(fmaf(sv[i], a.scale_log2, nm[c]));
         uint4 ph;
         ph.x = Ops::pack2(pr[0], pr[1]);
         ph.y = Ops::pack2(pr[2], pr[3]);
