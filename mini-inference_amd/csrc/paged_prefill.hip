@@ -110,15 +110,21 @@ struct PShape {
   static constexpr int TILE = kKT * RB;            // bytes of one K (or V) tile
   static constexpr int STAGE = 2 * TILE;           // K | V
   static constexpr int NLD = kKT * CPR / (kPW * kWave);  // 16-byte chunks per thread per tile, each of K and V
+  // V row r keeps its 16-byte chunk c at c ^ vsw(r). The XOR is even, so each 32-byte segment a
+  // transposing read takes stays whole, and the rows one such read touches (4 grp + 0..3 per
+  // 16 lanes, 8 rows per 32 lanes) start their segment in distinct banks of a 128-byte or a
+  // 256-byte bank window.
+  static __device__ __forceinline__ int vsw(int r) { return CPR >= 16 ? 2 * (r & 7) : 2 * ((r + (r >> 2)) & 3); }
   static_assert(NLD >= 1 && NLD * kPW * kWave == kKT * CPR, "tile must split evenly over the workgroup");
 };
 
 // One work item: new tokens [blk * TQ, blk * TQ + TQ) of sequence s against kv head kvh.
 // smem holds the two K | V stages, s_ok[stage][key] whether a key row is a real key (valid
-// block id). Called by the whole workgroup (the barriers inside are workgroup-wide).
+// block id), byte w of s_wok[stage] whether every key row wavefront w loaded is. Called by
+// the whole workgroup (the barriers inside are workgroup-wide).
 template <int DT, int D, int QR, int NC>
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int s, int blk, char* smem,
-                                             uint8_t (*s_ok)[kKT]) {
+                                             uint8_t (*s_ok)[kKT], uint32_t* s_wok) {
   using P = PShape<D>;
   using Ops = MfmaOps<DT>;
   constexpr int RB = P::RB, CPR = P::CPR, KC = P::KC, MT = P::MT;
@@ -214,9 +220,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
       const int idx = tid + j * kPW * kWave;
       const int r = idx / CPR, c = idx % CPR;
       *reinterpret_cast<uint4*>(st + r * RB + ((c ^ (r & (CPR - 1))) * 16)) = kbuf[j];  // K swizzled by row
-      *reinterpret_cast<uint4*>(st + P::TILE + r * RB + c * 16) = vbuf[j];
+      *reinterpret_cast<uint4*>(st + P::TILE + r * RB + ((c ^ P::vsw(r)) * 16)) = vbuf[j];
       if (c == 0) s_ok[stage][r] = okbuf[j];
     }
+    bool wok = true;
+#pragma unroll
+    for (int j = 0; j < P::NLD; ++j) wok = wok && okbuf[j];
+    wok = __all(wok);
+    if (lane == 0) reinterpret_cast<uint8_t*>(&s_wok[stage])[w] = wok ? 1 : 0;
   };
 
   f32x4_t acc[NC][MT];
@@ -266,23 +277,26 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
       // points at dims 16 mt + 4r .. +3 of key 4 grp + k, and lane i16 receives dim
       // 16 mt + i16 of keys 4 grp + 0..3 (then the same 16 keys later).
       uint4 vt[MT];
-      const char* vb = st + P::TILE + (4 * grp + (i16 >> 2)) * RB + (i16 & 3) * 8;
+      const int vrow = 4 * grp + (i16 >> 2), vs = P::vsw(vrow);  // rows vrow and vrow + 16 share vsw
+      const char* vb = st + P::TILE + vrow * RB + (i16 & 3) * 8;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const uint2 lo = lds_tr16(vb + 32 * mt);
-        const uint2 hi = lds_tr16(vb + 16 * RB + 32 * mt);
+        const int so = ((2 * mt) ^ vs) * 16;
+        const uint2 lo = lds_tr16(vb + so);
+        const uint2 hi = lds_tr16(vb + 16 * RB + so);
         vt[mt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
-      // The 8 keys of this lane's S^T halves: 4 grp + kr[i].
+      // The 8 keys of this lane's S^T halves: 4 grp + kr[i]. kok[i]: that key lies in a valid
+      // block (read per key only when some key of the tile does not).
       constexpr int kr[8] = {0, 1, 2, 3, 16, 17, 18, 19};
+      const bool allok = __builtin_amdgcn_readfirstlane(s_wok[stage]) == 0x01010101u;
       bool kok[8];
-      bool allok = true;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kok[i] = s_ok[stage][32 * h + 4 * grp + kr[i]] != 0;
-        allok = allok && kok[i];
+      for (int i = 0; i < 8; ++i) kok[i] = true;
+      if (!allok) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kok[i] = s_ok[stage][32 * h + 4 * grp + kr[i]] != 0;
       }
-      allok = __all(allok);  // every key of this 32-key step lies in a valid block
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         f32x4_t s0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
@@ -402,9 +416,11 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
   constexpr int TQ = kPW * NC * (16 / QR);
   __shared__ __attribute__((aligned(16))) char smem[2 * P::STAGE];
   __shared__ uint8_t s_ok[2][kKT];
+  __shared__ uint32_t s_wok[2];
+  static_assert(kPW == 4, "one byte per wavefront in s_wok");
   if constexpr (!PERSIST) {
     // One workgroup per (kv head, sequence, block), blocks of a sequence latest first.
-    prefill_item<DT, D, QR, NC>(a, blockIdx.x, blockIdx.y, gridDim.z - 1 - blockIdx.z, smem, s_ok);
+    prefill_item<DT, D, QR, NC>(a, blockIdx.x, blockIdx.y, gridDim.z - 1 - blockIdx.z, smem, s_ok, s_wok);
   } else {
     __shared__ int s_nb[kMaxSeqs];          // blocks of sequence s
     __shared__ int s_seq[kMaxSeqs];         // sequences by blocks, descending
@@ -460,7 +476,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
       const int seq = __builtin_amdgcn_readfirstlane(s_seq[rem / a.hkv]);
       const int kvh = __builtin_amdgcn_readfirstlane(rem % a.hkv);
       const int blk = __builtin_amdgcn_readfirstlane(zb - 1 - lo);
-      prefill_item<DT, D, QR, NC>(a, kvh, seq, blk, smem, s_ok);
+      prefill_item<DT, D, QR, NC>(a, kvh, seq, blk, smem, s_ok, s_wok);
     }
   }
 }
