@@ -180,6 +180,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
     for (int d = 1; d < kWave; d <<= 1) v = min(v, __shfl_xor(v, d));
     pmin[c] = __builtin_amdgcn_readfirstlane(v);
   }
+  int pmin_all = pmin[0];
+#pragma unroll
+  for (int c = 1; c < NC; ++c) pmin_all = pmin[c] < pmin_all ? pmin[c] : pmin_all;
 
   // ---- loader: this thread's K / V chunks of a tile. The block ids of a tile are read one
   // tile ahead of its rows, so the table lookup does not add a second latency per tile.
@@ -297,6 +300,11 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
 #pragma unroll
         for (int i = 0; i < 8; ++i) kok[i] = s_ok[stage][32 * h + 4 * grp + kr[i]] != 0;
       }
+      // Every column block's raw scores first, then one wave-uniform masking test and one
+      // rescale test for all of them, so that the exponentials and PV products of all blocks
+      // form one straight-line region the scheduler can interleave. Masked scores become -inf;
+      // only steps with a key past some row's position or in an invalid block need that.
+      float sv[NC][8];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         f32x4_t s0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
@@ -305,35 +313,49 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
           s0 = Ops::qk(kreg[0][kc], qreg[c][kc], s0);
           s1 = Ops::qk(kreg[1][kc], qreg[c][kc], s1);
         }
-        // Raw scores; masked ones become -inf, which only steps with a key past some row's
-        // position or in an invalid block need (a wave-uniform test).
-        float sv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sv[i] = i < 4 ? s0[i] : s1[i - 4];
-        if (!(allok && key0 + 31 <= pmin[c])) {
+        for (int i = 0; i < 8; ++i) sv[c][i] = i < 4 ? s0[i] : s1[i - 4];
+      }
+      if (!(allok && key0 + 31 <= pmin_all)) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
           // Key key0 + kr[i] + 4 grp is visible to this lane's row when kr[i] <= lim.
           const int lim = pos[c] - key0 - 4 * grp;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) sv[i] = (kok[i] && kr[i] <= lim) ? sv[i] : -INFINITY;
+          for (int i = 0; i < 8; ++i) sv[c][i] = (kok[i] && kr[i] <= lim) ? sv[c][i] : -INFINITY;
         }
-        // The rescale test on the lane's maximum, scaled once (the scale is positive).
-        const float mx = fmax3(fmax3(sv[0], sv[1], sv[2]), fmax3(sv[3], sv[4], sv[5]), fmax2(sv[6], sv[7])) *
-                         a.scale_log2;
-        if (__any(mx > mth[c])) {
-          const float mn = fmax2(m[c], max4(mx));
-          const float alpha = (m[c] == -INFINITY) ? 0.0f : fast_exp2(m[c] - mn);
-          l[c] *= alpha;
+      }
+      // The rescale test on each lane's maximum, scaled once (the scale is positive).
+      float mx[NC];
+      bool need = false;
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[c][mt] *= alpha;
-          m[c] = mn;
-          mth[c] = mn + kRescaleLog2;
-          // exp2(-inf - m) = 0 for any finite m; m stays -inf only while every score of the
-          // row so far is -inf, and then exp2(-inf - 0) = 0 as well.
-          nm[c] = mn == -INFINITY ? 0.0f : -mn;
+      for (int c = 0; c < NC; ++c) {
+        mx[c] = fmax3(fmax3(sv[c][0], sv[c][1], sv[c][2]), fmax3(sv[c][3], sv[c][4], sv[c][5]),
+                      fmax2(sv[c][6], sv[c][7])) * a.scale_log2;
+        need = need || mx[c] > mth[c];
+      }
+      if (__any(need)) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          if (__any(mx[c] > mth[c])) {
+            const float mn = fmax2(m[c], max4(mx[c]));
+            const float alpha = (m[c] == -INFINITY) ? 0.0f : fast_exp2(m[c] - mn);
+            l[c] *= alpha;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[c][mt] *= alpha;
+            m[c] = mn;
+            mth[c] = mn + kRescaleLog2;
+            // exp2(-inf - m) = 0 for any finite m; m stays -inf only while every score of the
+            // row so far is -inf, and then exp2(-inf - 0) = 0 as well.
+            nm[c] = mn == -INFINITY ? 0.0f : -mn;
+          }
         }
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
         float pr[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(fmaf(sv[i], a.scale_log2, nm[c]));
+        for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(fmaf(sv[c][i], a.scale_log2, nm[c]));
         uint4 ph;
         ph.x = Ops::pack2(pr[0], pr[1]);
         ph.y = Ops::pack2(pr[2], pr[3]);
