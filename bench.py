@@ -22,6 +22,8 @@ Reported (one JSON line on stdout):
                 (engine/cuda_graphs.py); decode_tok_s_eager: the same step launched eagerly
   prefill       packed prefill attention over a cached prefix (64 forks of a 520-token prefix,
                 suffixes U[32, 512], fp16): time per layer and TFLOP/s against the fp16 MFMA peak
+  long_context  the same append + attention step at 28 query / 4 KV heads, head_dim 128, bf16,
+                B=128, contexts log-uniform in [512, 8192], block 32: time per layer and GB/s
   cpu_baseline  the reference's torch CPU path (index_put_ append + table gather + SDPA,
                 the oracle's restatement) timed on this host's cores for one layer, fp32
 
@@ -120,6 +122,89 @@ def cpu_baseline(batch, layer_q, layer_k, layer_v, budget_s: float) -> dict:
         model = "unknown"
     return {"per_layer_s": per_layer, "runs": len(timed), "warmup": min(warm, len(times)), "cores": cores,
             "cpu_model": model}
+
+
+def decode_step(batch, dev, calls_per_step: int | None = None):
+    """One decode step over every layer of ``batch``'s cache, as PagedDecodeContext.attend
+    issues it: the step's work plan once, then per layer one fused append + attention call
+    (``mip_paged_decode_append``) with distinct per-layer q/k/v. With ``calls_per_step`` the
+    step makes that many calls, cycling over the cache's layers. Returns the step and the
+    per-layer (q, k, v) lists."""
+    import torch
+
+    from engine import paged_ops, workloads
+
+    shape, cache = batch.shape, batch.cache
+    layers = shape.num_layers
+    qs, ks, vs = [], [], []
+    for layer in range(layers):
+        q, k, v = workloads.step_inputs(batch, seed=100 + layer)
+        qs.append(q)
+        ks.append(k)
+        vs.append(v)
+    ctx = cache.decode_context(batch.slots)
+    outs = [torch.empty(shape.batch, shape.num_heads, shape.head_dim, dtype=shape.dtype, device=dev)
+            for _ in range(layers)]
+    plan_call, plan = paged_ops.prepare_decode_plan(ctx.context_lens, ctx.block_tables, shape.num_heads,
+                                                    shape.num_kv_heads, shape.head_dim, shape.block_size, shape.dtype,
+                                                    max_blocks=ctx.num_blocks)
+    calls = [paged_ops.prepare_paged_decode(qs[i][:, :, 0], cache.k[i], cache.v[i], ctx.block_tables,
+                                            ctx.context_lens, ctx.scale, out=outs[i], max_blocks=ctx.num_blocks,
+                                            append=(ks[i][:, :, 0], vs[i][:, :, 0], ctx.slot_mapping), plan=plan)[0]
+             for i in range(layers)]
+
+    n_calls = layers if calls_per_step is None else calls_per_step
+
+    def hot_step():
+        if plan_call is not None:
+            plan_call()  # once per step: the work split every layer shares
+        for i in range(n_calls):
+            calls[i % layers]()
+
+    return hot_step, (qs, ks, vs)
+
+
+def long_context_measure(dev, steps: int = 10, layers: int = 4) -> dict:
+    """Append + decode attention at the long-context shape: 28 query / 4 KV heads, head_dim
+    128, bf16, batch 128, contexts log-uniform in [512, 8192], block size 32, the pool churned
+    by 5,000 alloc/free events. A step is the plan plus 28 fused calls (one per layer of the
+    model), cycling over ``layers`` distinct layers of the pool (every layer's work is the
+    same; 4 layers keep the K/V the calls read, 3.3 GB, far above the 256 MB last-level
+    cache). HIP events; the figure is the step time over 28."""
+    import dataclasses
+
+    import torch
+
+    from engine import workloads
+
+    shape = dataclasses.replace(workloads.SHAPES[5], num_layers=layers)
+    batch = workloads.build_decode_batch(shape, dev, seed=0)
+    n_calls = workloads.SHAPES[5].num_layers
+    step, _ = decode_step(batch, dev, calls_per_step=n_calls)
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t = time_loop(step, steps) / n_calls
+    lens = [n + 1 for n in batch.ctx]
+    nbytes = attention_bytes(lens, shape) + append_bytes(shape)
+    gbps = nbytes / t / 1e9
+    del batch, step
+    torch.cuda.empty_cache()
+    return {
+        "workload": "paged decode step (KV append + paged attention), 28q/4kv heads d128, bf16, B=128, ctx "
+                    f"log-uniform[512,8192], block 32, churned pool; plan + 28 calls per step over {layers} "
+                    "distinct layers",
+        "kernel": "paged_decode_stream_tiles<bf16, D=128, QR=8, NS=3> (planned, with the fused append) + "
+                  "paged_decode_stream_merge<bf16, D=128>",
+        "us_per_layer": round(t * 1e6, 2),
+        "bound": "hbm",
+        "achieved": round(gbps, 1),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "bytes_per_layer": nbytes,
+        "mean_ctx": round(statistics.mean(lens) - 1, 1),
+    }
 
 
 def decode_tok_s(batch, steps: int, warmup: int) -> dict:
@@ -331,6 +416,8 @@ def main() -> int:
     ap.add_argument("--no-model", action="store_true", help="skip the full-model decode tok/s measurement")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the packed prefill attention, packed append and block-copy measurements")
+    ap.add_argument("--no-long-context", action="store_true",
+                    help="skip the long-context decode measurement (28q/4kv heads d128, B=128, ctx up to 8192)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 512 MiB device copy three times (HBM counter scale for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -363,31 +450,8 @@ def main() -> int:
     log(f"workload ready in {time.perf_counter() - t0:.1f}s: B={shape.batch} layers={shape.num_layers} "
         f"pool={cache.num_blocks} blocks, mean ctx {statistics.mean(batch.ctx):.0f}")
 
-    # Per-layer step inputs (distinct per layer) and one decode context for the step.
     layers = shape.num_layers
-    qs, ks, vs = [], [], []
-    for layer in range(layers):
-        q, k, v = workloads.step_inputs(batch, seed=100 + layer)
-        qs.append(q)
-        ks.append(k)
-        vs.append(v)
-    ctx = cache.decode_context(batch.slots)
-    outs = [torch.empty(shape.batch, shape.num_heads, shape.head_dim, dtype=shape.dtype, device=dev)
-            for _ in range(layers)]
-    plan_call, plan = paged_ops.prepare_decode_plan(ctx.context_lens, ctx.block_tables, shape.num_heads,
-                                                    shape.num_kv_heads, shape.head_dim, shape.block_size, shape.dtype,
-                                                    max_blocks=ctx.num_blocks)
-    calls = [paged_ops.prepare_paged_decode(qs[i][:, :, 0], cache.k[i], cache.v[i], ctx.block_tables,
-                                            ctx.context_lens, ctx.scale, out=outs[i], max_blocks=ctx.num_blocks,
-                                            append=(ks[i][:, :, 0], vs[i][:, :, 0], ctx.slot_mapping), plan=plan)[0]
-             for i in range(layers)]
-
-    def hot_step():
-        if plan_call is not None:
-            plan_call()  # once per step: the work split all 24 layers share
-        for i in range(layers):
-            calls[i]()
-
+    hot_step, (qs, ks, vs) = decode_step(batch, dev)
     for _ in range(args.warmup):
         hot_step()
     torch.cuda.synchronize()
@@ -479,6 +543,15 @@ def main() -> int:
         except Exception as exc:
             log(f"block copy measurement failed: {exc!r}")
             result["block_copy"] = None
+
+    if not args.no_long_context:
+        try:
+            result["long_context"] = long_context_measure(dev)
+            lc = result["long_context"]
+            log(f"long-context decode: {lc['us_per_layer']} us/layer, {lc['achieved']} GB/s ({lc['frac']:.1%} of peak)")
+        except Exception as exc:
+            log(f"long-context decode measurement failed: {exc!r}")
+            result["long_context"] = None
 
     if not args.no_cpu_baseline:
         cb = cpu_baseline(batch, qs[0], ks[0], vs[0], args.cpu_budget)
