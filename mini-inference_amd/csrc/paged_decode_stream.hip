@@ -826,9 +826,15 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
   wait_vmcnt<0>();  // no direct load may land in LDS after this wavefront ends
 }
 
-// Combine the pieces of every segment the stream kernel split. Grid (kv heads, batch).
-template <int DT, int D, bool FUSED, bool PLANNED>
-__global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) {
+// Combine the pieces of every segment the stream kernel split. Grid (kv heads, batch),
+// NSTR * 256 threads: NSTR streams of 256 threads take alternate chunks of 16 pieces (each
+// stream with its own online maximum), and stream 0 then combines the streams' states in
+// stream order. NSTR = 1 serves batches of many segments (each segment has few pieces);
+// NSTR = 2 serves a few long sequences, whose segments have up to a few hundred pieces (two
+// streams keep a chunk's 16 partial sums per thread in registers: at 1024 threads a thread
+// has 128 registers, and the chunk buffer alone takes 128).
+template <int DT, int D, bool FUSED, bool PLANNED, int NSTR>
+__global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamArgs sa) {
   using S = typename Elem<DT>::S;
   const int64_t REC = sa.rec_stride;
   const DecodeArgs& a = sa.a;
@@ -891,14 +897,17 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
   auto rec_of = [&](int r) -> const float* {
     return sa.ws_rec + (static_cast<int64_t>(gw_lo + r) * 2 + (r == 0 && lo_split ? 1 : 0)) * REC;
   };
-  // One pass over chunks of 16 records with an online maximum per row. Every thread owns up
+  // Passes over chunks of 16 records with an online maximum per row. Every thread owns up
   // to two quads of four output columns of one row; the quads' partial sums of a chunk are
   // loaded together with the chunk's (m, l) pairs, so a chunk costs one memory round trip.
+  // Stream str takes chunks str, str + NSTR, ... (a round count uniform over the workgroup,
+  // so every thread reaches every barrier).
   constexpr int kRC = 16;
   constexpr int Q = D / 4;  // column quads per row
-  __shared__ float s_m[kRC][16];
-  __shared__ float s_l[kRC][16];
-  const int t = threadIdx.x, tg = t & 15, tr = t >> 4;
+  __shared__ float s_m[NSTR][kRC][16];
+  __shared__ float s_l[NSTR][kRC][16];
+  const int str = static_cast<int>(threadIdx.x) / 256;
+  const int t = threadIdx.x % 256, tg = t & 15, tr = t >> 4;
   const int nq = G * Q;  // quads per (kv head, sequence): at most 512
   const int nj = nq > 256 ? 2 : 1;
   float4 acc[2];
@@ -909,8 +918,10 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
     mrun[j] = -INFINITY;
     lrun[j] = 0.0f;
   }
-  for (int c0 = 0; c0 < R; c0 += kRC) {
-    const int nr = R - c0 < kRC ? R - c0 : kRC;
+  const int rounds = ((R + kRC - 1) / kRC + NSTR - 1) / NSTR;
+  for (int rd = 0; rd < rounds; ++rd) {
+    const int c0 = (rd * NSTR + str) * kRC;
+    const int nr = c0 >= R ? 0 : (R - c0 < kRC ? R - c0 : kRC);  // 0: this stream has no chunk this round
     float4 v[2][kRC];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -928,29 +939,29 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
       mp = rec[tg];
       lp = rec[16 + tg];
     }
-    s_m[tr][tg] = mp;
-    s_l[tr][tg] = lp;
+    s_m[str][tr][tg] = mp;
+    s_l[str][tr][tg] = lp;
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int qd = t + 256 * j;
-      if (j < nj && qd < nq) {
+      if (nr > 0 && j < nj && qd < nq) {
         const int g = qd / Q;
         float cm = mrun[j];
-        for (int k = 0; k < nr; ++k) cm = fmaxf(cm, s_m[k][g]);
+        for (int k = 0; k < nr; ++k) cm = fmaxf(cm, s_m[str][k][g]);
         const float alpha = mrun[j] == -INFINITY ? 0.0f : fast_exp2(mrun[j] - cm);
         float4 s = make_float4(acc[j].x * alpha, acc[j].y * alpha, acc[j].z * alpha, acc[j].w * alpha);
         float ls = lrun[j] * alpha;
 #pragma unroll
         for (int k = 0; k < kRC; ++k)
           if (k < nr) {
-            const float mk = s_m[k][g];
+            const float mk = s_m[str][k][g];
             const float wk = mk == -INFINITY ? 0.0f : fast_exp2(mk - cm);
             s.x = fmaf(wk, v[j][k].x, s.x);
             s.y = fmaf(wk, v[j][k].y, s.y);
             s.z = fmaf(wk, v[j][k].z, s.z);
             s.w = fmaf(wk, v[j][k].w, s.w);
-            ls = fmaf(wk, s_l[k][g], ls);
+            ls = fmaf(wk, s_l[str][k][g], ls);
           }
         acc[j] = s;
         lrun[j] = ls;
@@ -958,6 +969,43 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(StreamArgs sa) 
       }
     }
     __syncthreads();  // the next chunk overwrites s_m / s_l
+  }
+  if constexpr (NSTR > 1) {
+    // Streams 1.. hand their state to stream 0, which folds them in stream order with weights
+    // exp2(m_s - M), M the largest m_s (an empty stream, m = -inf, weighs 0).
+    __shared__ float4 s_acc[NSTR - 1][2][256];
+    __shared__ float2 s_ml[NSTR - 1][2][256];
+    if (str > 0) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        s_acc[str - 1][j][t] = acc[j];
+        s_ml[str - 1][j][t] = make_float2(mrun[j], lrun[j]);
+      }
+    }
+    __syncthreads();
+    if (str > 0) return;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float mm = mrun[j];
+#pragma unroll
+      for (int u = 0; u < NSTR - 1; ++u) mm = fmaxf(mm, s_ml[u][j][t].x);
+      const float w0 = mrun[j] == -INFINITY ? 0.0f : fast_exp2(mrun[j] - mm);
+      float4 s = make_float4(acc[j].x * w0, acc[j].y * w0, acc[j].z * w0, acc[j].w * w0);
+      float ls = lrun[j] * w0;
+#pragma unroll
+      for (int u = 0; u < NSTR - 1; ++u) {
+        const float2 ml = s_ml[u][j][t];
+        const float4 a4 = s_acc[u][j][t];
+        const float wu = ml.x == -INFINITY ? 0.0f : fast_exp2(ml.x - mm);
+        s.x = fmaf(wu, a4.x, s.x);
+        s.y = fmaf(wu, a4.y, s.y);
+        s.z = fmaf(wu, a4.z, s.z);
+        s.w = fmaf(wu, a4.w, s.w);
+        ls = fmaf(wu, ml.y, ls);
+      }
+      acc[j] = s;
+      lrun[j] = ls;
+    }
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -1093,7 +1141,7 @@ using StreamFn = void (*)(StreamArgs);
 
 struct StreamPick {
   StreamFn main[2][2] = {};   // [fused: with the step's K/V append][planned: from a work plan]
-  StreamFn merge[2][2] = {};
+  StreamFn merge[2][2][2] = {};  // [fused][planned][2 streams: a few long segments]
   int ring_bytes = 0;  // per wavefront
 };
 
@@ -1105,10 +1153,14 @@ StreamPick pick_one() {
   p.main[0][1] = paged_decode_stream_tiles<DT, D, QR, NS, false>;
   p.main[1][0] = paged_decode_stream<DT, D, QR, NS, true>;
   p.main[1][1] = paged_decode_stream_tiles<DT, D, QR, NS, true>;
-  p.merge[0][0] = paged_decode_stream_merge<DT, D, false, false>;
-  p.merge[0][1] = paged_decode_stream_merge<DT, D, false, true>;
-  p.merge[1][0] = paged_decode_stream_merge<DT, D, true, false>;
-  p.merge[1][1] = paged_decode_stream_merge<DT, D, true, true>;
+  p.merge[0][0][0] = paged_decode_stream_merge<DT, D, false, false, 1>;
+  p.merge[0][1][0] = paged_decode_stream_merge<DT, D, false, true, 1>;
+  p.merge[1][0][0] = paged_decode_stream_merge<DT, D, true, false, 1>;
+  p.merge[1][1][0] = paged_decode_stream_merge<DT, D, true, true, 1>;
+  p.merge[0][0][1] = paged_decode_stream_merge<DT, D, false, false, 2>;
+  p.merge[0][1][1] = paged_decode_stream_merge<DT, D, false, true, 2>;
+  p.merge[1][0][1] = paged_decode_stream_merge<DT, D, true, false, 2>;
+  p.merge[1][1][1] = paged_decode_stream_merge<DT, D, true, true, 2>;
   p.ring_bytes = NS * Ring<D, QR>::STAGE;
   return p;
 }
@@ -1133,9 +1185,18 @@ int stream_min_tiles() {
   return 4;
 }
 
+// Calls with at most this many segments (batch x kv heads) merge with 2 streams per
+// workgroup: a few long sequences, whose segments are split into tens of pieces each
+// (B=1 at 32k keys: 29.2 -> 26.4 us per call, B=4 at 8k: 18.2 -> 15.1 us, B=16 at 16k:
+// 37.1 -> 34.2 us). Batches of more segments have a handful of pieces per segment.
+constexpr int64_t kWideMergeSegments = 64;
+int stream_wide_merge(int64_t segments) { return segments <= kWideMergeSegments ? 1 : 0; }
+
 // Most pieces per segment on average (see stream_active_waves). 64 measured best for one to
-// four long sequences (B=1 at 32k keys: 74 -> 32 us per call; 128: 31 us, 256: 42 us, 32:
-// 46 us) and leaves batches of hundreds of sequences untouched.
+// four long sequences, with either merge (one-stream merge, B=1 at 32k keys: 74 -> 32 us per
+// call; 128: 31 us, 256: 42 us, 32: 46 us; two-stream merge: 26.4 us, 128: 23.3 us but B=4
+// at 8k 18.6 against 15.1 us, 256: 29.7 us) and leaves batches of hundreds of sequences
+// untouched.
 int stream_max_pieces() {
   if (const char* env = std::getenv("MIP_STREAM_MAX_PIECES")) {
     const int v = std::atoi(env);
@@ -1177,7 +1238,9 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, i
   sa.rec_stride = static_cast<int>(cfg.rec_floats);
   const int fused = sa.app.slots != nullptr, planned = sa.plan != nullptr;
   hipLaunchKernelGGL(p.main[fused][planned], dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
-  hipLaunchKernelGGL(p.merge[fused][planned], dim3(num_kv_heads, batch), dim3(256), 0, stream, sa);
+  const int wide = stream_wide_merge(static_cast<int64_t>(batch) * num_kv_heads);
+  hipLaunchKernelGGL(p.merge[fused][planned][wide], dim3(num_kv_heads, batch), dim3(wide ? 512 : 256), 0, stream,
+                     sa);
   return static_cast<int>(hipGetLastError());
 }
 

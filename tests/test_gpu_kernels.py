@@ -387,6 +387,28 @@ def test_paged_decode_edge_batches(gpu):
     assert attention_error(values(out), want, "float16") <= TOL["float16"]
 
 
+@pytest.mark.parametrize("batch", [32, 33, 40])
+def test_paged_decode_merge_streams(gpu, batch):
+    """One long sequence among short ones: its segments split into many pieces. At batch 32
+    (64 segments) the merge runs two streams per workgroup, at 33 and 40 one; both against
+    float64, and the planned call bit-identical to the one deriving its split in-kernel."""
+    from engine import paged_ops
+
+    announce(f"paged_decode merge streams B={batch}")
+    lens = [20000] + [17 + (i * 53) % 190 for i in range(batch - 1)]
+    q, k_pool, v_pool, tables, bt, width = _random_case("bfloat16", batch, 14, 2, 64, 16, lens, seed=31 + batch)
+    qg, kg, vg = q.to(gpu), k_pool.to(gpu), v_pool.to(gpu)
+    bt_t = torch.from_numpy(bt).to(gpu)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=gpu)
+    out0 = paged_ops.paged_decode(qg, kg, vg, bt_t, lens_t, max_blocks=width)
+    plan = paged_ops.decode_plan(lens_t, bt_t, 14, 2, 64, 16, DTYPES["bfloat16"], max_blocks=width)
+    out1 = paged_ops.paged_decode(qg, kg, vg, bt_t, lens_t, max_blocks=width, plan=plan)
+    torch.cuda.synchronize()
+    want = ref.attention_f64(values(q), values(k_pool), values(v_pool), tables, lens, 16)
+    assert attention_error(values(out0), want, "bfloat16") <= TOL["bfloat16"]
+    assert torch.equal(out0, out1)
+
+
 def test_paged_decode_large_logits_rescale(gpu):
     """Scores spanning hundreds of units exercise the lazy running-max rescale."""
     from engine import paged_ops
