@@ -25,8 +25,9 @@
 // a key mask it out; a wavefront skips tiles that lie beyond all of its rows' positions, and a
 // column block skips the masking in steps whose keys all of its live rows see (most of them).
 // The kernel is VALU-bound, so the softmax step is kept short: the rescale test on each lane's
-// maximum, the scale folded into the exponent's fma, and (fp16) the row sums taken from the
-// packed fp16 weights with v_dot2; V^T comes from transposing LDS reads.
+// maximum, the scale folded into the exponent's fma, and the row sums taken on the matrix
+// cores (the weights against a block of ones, one more 16x16x32 product per column block);
+// V^T comes from transposing LDS reads.
 #include "paged_decode_common.h"
 
 namespace mip {
@@ -67,12 +68,6 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-__device__ __forceinline__ float sum4(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
 // Maxima by IEEE 754-2019 maximum (v_maximum3_f32 on gfx950). fmaxf (maxNum) has to quiet
 // signalling NaNs in IEEE mode, which costs one extra v_max per operand that is not the
 // result of arithmetic (MFMA outputs, lane exchanges); maximum needs no such step. The two
@@ -210,7 +205,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
       const bool ok = key <= p_last && bok;
       // Keys past the last position re-read that position's row (a real key, so finite V: the
       // PV product multiplies every row of the tile, masked or not).
-      const int64_t row = (static_cast<int64_t>(bok ? b : 0) * a.hkv + kvh) * a.bs + (kk & (a.bs - 1));
+      // Pool row (block b, head kvh, offset): one 32 x 32 -> 64-bit multiply-add.
+      const uint64_t row = static_cast<uint64_t>(bok ? static_cast<uint32_t>(b) : 0u) * static_cast<uint32_t>(a.hkv * a.bs) +
+                           static_cast<uint32_t>(kvh * a.bs + (kk & (a.bs - 1)));
       kbuf[j] = *reinterpret_cast<const uint4*>(a.k + row * RB + c * 16);
       vbuf[j] = *reinterpret_cast<const uint4*>(a.v + row * RB + c * 16);
       okbuf[j] = ok;
@@ -234,14 +231,15 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
   };
 
   f32x4_t acc[NC][MT];
-  float m[NC], l[NC];
+  f32x4_t lacc[NC];  // row sums by MFMA against a ones block: every element holds row i16's sum
+  float m[NC];
   float mth[NC], nm[NC];  // m + kRescaleLog2 (the rescale threshold) and -m (0 while m = -inf)
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     m[c] = -INFINITY;
     mth[c] = -INFINITY;
     nm[c] = 0.0f;
-    l[c] = 0.0f;
+    lacc[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[c][mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   }
@@ -340,7 +338,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
           if (__any(mx[c] > mth[c])) {
             const float mn = fmax2(m[c], max4(mx[c]));
             const float alpha = (m[c] == -INFINITY) ? 0.0f : fast_exp2(m[c] - mn);
-            l[c] *= alpha;
+            lacc[c] *= alpha;
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[c][mt] *= alpha;
             m[c] = mn;
@@ -361,17 +359,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
         ph.y = Ops::pack2(pr[2], pr[3]);
         ph.z = Ops::pack2(pr[4], pr[5]);
         ph.w = Ops::pack2(pr[6], pr[7]);
-        if constexpr (kSplitP<DT>) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) l[c] += pr[i];
-        } else {
-          // Row sum of the fp16 weights the PV product uses: packed pairs against (1, 1).
-          constexpr uint32_t kOnes = 0x3c003c00u;
-          l[c] = dot2<DT>(ph.x, kOnes, l[c]);
-          l[c] = dot2<DT>(ph.y, kOnes, l[c]);
-          l[c] = dot2<DT>(ph.z, kOnes, l[c]);
-          l[c] = dot2<DT>(ph.w, kOnes, l[c]);
-        }
+        // Row sums of the weights the PV product uses, on the matrix cores.
+        constexpr uint32_t kOne2 = DT == MIP_BF16 ? 0x3f803f80u : 0x3c003c00u;
+        const uint4 ones = make_uint4(kOne2, kOne2, kOne2, kOne2);
+        lacc[c] = Ops::qk(ones, ph, lacc[c]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[c][mt] = Ops::qk(vt[mt], ph, acc[c][mt]);
         if constexpr (kSplitP<DT>) {
@@ -383,6 +374,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
           pl.w = Ops::pack2(pr[6] - Ops::lo(ph.w), pr[7] - Ops::hi(ph.w));
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) acc[c][mt] = Ops::qk(vt[mt], pl, acc[c][mt]);
+          lacc[c] = Ops::qk(ones, pl, lacc[c]);
         }
       }
     }
@@ -395,7 +387,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
   using S = typename Elem<DT>::S;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const float lt = sum4(l[c]);
+    const float lt = lacc[c][0];
     if (!live[c]) continue;
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     const int tok = tok_lo + (w * NC + c) * TPC + i16 / QR;
