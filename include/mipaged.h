@@ -131,7 +131,8 @@ int mip_rope_kv_append(void* q, int64_t q_stride_tok, int64_t q_stride_head,
  * clamped to it).
  *
  * `workspace` is scratch device memory for split contexts (per-piece softmax state and
- * partial outputs, combined by a second kernel on the same stream). It must hold
+ * partial outputs, combined by a second kernel on the same stream; for a batch of at most
+ * 16 sequence x kv-head segments, a third kernel folds the second's per-run states). It must hold
  * mip_paged_decode_workspace(...) bytes for the same shape, asked with the same device
  * current, and be 256-byte aligned. It needs no initialisation and its contents are
  * undefined afterwards; calls on one stream may reuse it, calls that can run

@@ -689,7 +689,7 @@ struct WsLayout {
   int nparts;
   int64_t ml_off, acc_off, bytes;
   StreamConfig stream;          // stream kernel launch shape
-  int64_t prefix_off, rec_off;  // stream kernel workspace
+  int64_t prefix_off, rec_off, part_off;  // stream kernel workspace
 };
 
 WsLayout ws_layout(int batch, int hq, int hkv, int d, int bs, int max_blocks, int dtype) {
@@ -702,7 +702,8 @@ WsLayout ws_layout(int batch, int hq, int hkv, int d, int bs, int max_blocks, in
     } else {
       w.prefix_off = 0;
       w.rec_off = align_up(static_cast<int64_t>(batch + 1) * 4, 256);
-      w.bytes = w.rec_off + align_up(static_cast<int64_t>(w.stream.tw) * 2 * w.stream.rec_floats * 4, 256);
+      w.part_off = w.rec_off + align_up(static_cast<int64_t>(w.stream.tw) * 2 * w.stream.rec_floats * 4, 256);
+      w.bytes = w.part_off + align_up(stream_part_floats(w.stream, batch, hkv) * 4, 256);
       w.nparts = 1;
       return w;
     }
@@ -899,6 +900,7 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
     sa.group = group;
     sa.ws_prefix = reinterpret_cast<int*>(static_cast<char*>(workspace) + wl.prefix_off);
     sa.ws_rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.rec_off);
+    sa.ws_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_off);
     sa.app = app;
     // A plan drives the tile-descriptor kernel, which needs tiles inside one block and 32-bit
     // lane offsets into the q head rows; otherwise the kernel derives its split itself.

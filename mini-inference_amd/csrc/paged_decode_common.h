@@ -108,6 +108,11 @@ struct StreamArgs {
   int rec_stride;  // floats per record: m[16] | l[16] | acc[group][D]
   int* ws_prefix;  // [batch + 1] tile prefix over sequences (written by workgroup 0)
   float* ws_rec;   // [tw][2][rec_stride]
+  // Calls with few segments: the merge cuts a segment of many pieces into `parts` runs (one
+  // workgroup each) and leaves their states here, [batch * kv heads][parts][rec_stride], for
+  // the fold kernel. parts = 1: the merge combines every segment whole.
+  float* ws_part;
+  int parts;
 };
 
 template <int D>
@@ -172,6 +177,8 @@ struct StreamConfig {
   int64_t rec_floats;
 };
 StreamConfig stream_config(int dtype, int d, int group, int batch);
+// Floats of second-level merge records a call of this shape needs (0: it merges in one pass).
+int64_t stream_part_floats(const StreamConfig& cfg, int batch, int num_kv_heads);
 int stream_launch(const StreamConfig& cfg, const StreamArgs& sa, int dtype, int d, int group, int num_kv_heads,
                   int batch, hipStream_t stream);
 // Bytes of a work plan for this launch shape (0: no plan, block size < 16), and the plan kernel.

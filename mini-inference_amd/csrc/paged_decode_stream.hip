@@ -826,6 +826,12 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
   wait_vmcnt<0>();  // no direct load may land in LDS after this wavefront ends
 }
 
+// Pieces per merge chunk (one memory round trip), streams of the merge for calls with few
+// segments, and the runs a long segment of such a call is cut into.
+constexpr int kMergeChunk = 16;
+constexpr int kWideMergeStreams = 2;
+constexpr int kStreamParts = 16;
+
 // Combine the pieces of every segment the stream kernel split. Grid (kv heads, batch),
 // NSTR * 256 threads: NSTR streams of 256 threads take alternate chunks of 16 pieces (each
 // stream with its own online maximum), and stream 0 then combines the streams' states in
@@ -839,13 +845,14 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
   const int64_t REC = sa.rec_stride;
   const DecodeArgs& a = sa.a;
   const int kvh = blockIdx.x, b = blockIdx.y, G = sa.group;
+  const int z = blockIdx.z, Z = gridDim.z;  // run z of Z of a parted segment
   S* out_base = reinterpret_cast<S*>(a.out);
   const int cap = a.max_blocks * a.bs;
   // Fused append: copy sequence b's new K and V rows of this kv head into the pool. The
   // stream kernel, which ran before this one, took the newest key straight from the source,
   // so nothing reads these pool rows in this call.
   const AppendRows& ap = sa.app;
-  if (FUSED && threadIdx.x < 2 * (D * 2 / 16)) {
+  if (FUSED && z == 0 && threadIdx.x < 2 * (D * 2 / 16)) {
     constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
     const int side = threadIdx.x / CPR, c = threadIdx.x % CPR;
     const int64_t slot = ap.slots[b];
@@ -874,9 +881,10 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
     L = L < cap ? L : cap;
   }
   if (L <= 0) {
-    for (int i = threadIdx.x; i < G * D; i += blockDim.x)
-      out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + i / D) * a.out_sh + i % D] =
-          from_f32<DT>(0.0f);
+    if (z == 0)
+      for (int i = threadIdx.x; i < G * D; i += blockDim.x)
+        out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + i / D) * a.out_sh + i % D] =
+            from_f32<DT>(0.0f);
     return;
   }
   if constexpr (!PLANNED) {
@@ -891,6 +899,19 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
   }
   if (gw_lo >= gw_hi) return;  // one wavefront held the whole segment and wrote it
   const int R = gw_hi - gw_lo + 1;
+  // A segment of more than one round of chunks, with Z > 1, is cut into Z runs of consecutive
+  // pieces [p0, p0 + np), one per workgroup z; each leaves its state in a second-level record
+  // that paged_decode_stream_fold combines. Otherwise workgroup 0 merges the whole segment.
+  const bool parted = Z > 1 && R > NSTR * kMergeChunk;
+  int p0 = 0, np = R;
+  if (parted) {
+    const int P = (R + Z - 1) / Z;
+    p0 = z * P;
+    if (p0 >= R) return;
+    np = R - p0 < P ? R - p0 : P;
+  } else if (z > 0) {
+    return;
+  }
   // Record r of this segment: the first piece sits in the "last segment" slot of wavefront
   // gw_lo when that wavefront started inside an earlier segment, every other piece in the
   // "first segment" slot of its wavefront.
@@ -902,7 +923,7 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
   // loaded together with the chunk's (m, l) pairs, so a chunk costs one memory round trip.
   // Stream str takes chunks str, str + NSTR, ... (a round count uniform over the workgroup,
   // so every thread reaches every barrier).
-  constexpr int kRC = 16;
+  constexpr int kRC = kMergeChunk;
   constexpr int Q = D / 4;  // column quads per row
   __shared__ float s_m[NSTR][kRC][16];
   __shared__ float s_l[NSTR][kRC][16];
@@ -918,10 +939,10 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
     mrun[j] = -INFINITY;
     lrun[j] = 0.0f;
   }
-  const int rounds = ((R + kRC - 1) / kRC + NSTR - 1) / NSTR;
+  const int rounds = ((np + kRC - 1) / kRC + NSTR - 1) / NSTR;
   for (int rd = 0; rd < rounds; ++rd) {
-    const int c0 = (rd * NSTR + str) * kRC;
-    const int nr = c0 >= R ? 0 : (R - c0 < kRC ? R - c0 : kRC);  // 0: this stream has no chunk this round
+    const int c0 = p0 + (rd * NSTR + str) * kRC;  // first piece of this stream's chunk
+    const int nr = c0 >= p0 + np ? 0 : (p0 + np - c0 < kRC ? p0 + np - c0 : kRC);  // 0: no chunk this round
     float4 v[2][kRC];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -1005,7 +1026,25 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
       }
       acc[j] = s;
       lrun[j] = ls;
+      mrun[j] = mm;  // the folded state is relative to mm (a run record stores it)
     }
+  }
+  if (parted) {
+    // Second-level record of run z: m[16] | l[16] | acc[G][D], as the stream kernel's records.
+    float* rec = sa.ws_part + ((static_cast<int64_t>(b) * a.hkv + kvh) * Z + z) * REC;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int qd = t + 256 * j;
+      if (j < nj && qd < nq) {
+        const int g = qd / Q, col = (qd % Q) * 4;
+        *reinterpret_cast<float4*>(rec + 32 + g * D + col) = acc[j];
+        if (col == 0) {
+          rec[g] = mrun[j];
+          rec[16 + g] = lrun[j];
+        }
+      }
+    }
+    return;
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -1019,6 +1058,79 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
       o[2] = from_f32<DT>(acc[j].z * inv);
       o[3] = from_f32<DT>(acc[j].w * inv);
     }
+  }
+}
+
+// Second level of the merge for calls with few segments: combines the kStreamParts run
+// states the merge left for every parted segment, in run order with weights exp2(m_z - M),
+// M the largest m_z. Grid (kv heads, batch); segments the merge combined whole are skipped.
+template <int DT, int D, bool PLANNED>
+__global__ __launch_bounds__(256) void paged_decode_stream_fold(StreamArgs sa) {
+  using S = typename Elem<DT>::S;
+  const int64_t REC = sa.rec_stride;
+  const DecodeArgs& a = sa.a;
+  const int kvh = blockIdx.x, b = blockIdx.y, G = sa.group, Z = sa.parts;
+  int L, gw_lo, gw_hi;
+  if constexpr (PLANNED) {
+    const int32_t* sd = sa.plan + sa.plan_seg_off + (static_cast<int64_t>(b) * a.hkv + kvh) * kPlanSeg;
+    const int pb = load_uniform_i32(sa.plan + 2), ph = load_uniform_i32(sa.plan + 3);
+    const int ps = load_uniform_i32(sa.plan + kPlanSegOffWord);
+    gw_lo = load_uniform_i32(sd + 0);
+    gw_hi = gw_lo + load_uniform_i32(sd + 1) - 1;
+    L = load_uniform_i32(sd + 3);
+    if (pb != sa.batch || ph != a.hkv || ps != sa.plan_seg_off || gw_lo < 0 || gw_hi >= sa.tw) return;
+  } else {
+    const int cap = a.max_blocks * a.bs;
+    L = a.lens[b];
+    L = L < cap ? L : cap;
+    if (L <= 0) return;
+    const int total = a.hkv * sa.ws_prefix[sa.batch];
+    const int tw = stream_active_waves(sa.tw, total, sa.min_tiles, static_cast<int64_t>(sa.batch) * a.hkv, sa.max_pieces);
+    const int n = (L + 15) >> 4;
+    const int64_t s0 = static_cast<int64_t>(a.hkv) * sa.ws_prefix[b] + static_cast<int64_t>(kvh) * n;
+    gw_lo = static_cast<int>(((s0 + 1) * tw - 1) / total);
+    gw_hi = static_cast<int>(((s0 + n) * tw - 1) / total);
+  }
+  const int R = gw_hi - gw_lo + 1;
+  if (L <= 0 || Z <= 1 || R <= kWideMergeStreams * kMergeChunk) return;  // merged whole
+  const int P = (R + Z - 1) / Z, nz = (R + P - 1) / P;
+  const float* base = sa.ws_part + (static_cast<int64_t>(b) * a.hkv + kvh) * Z * REC;
+  constexpr int Q = D / 4;
+  const int nq = G * Q;
+  for (int qd = threadIdx.x; qd < nq; qd += blockDim.x) {
+    const int g = qd / Q, col = (qd % Q) * 4;
+    float mz[kStreamParts], lz[kStreamParts];
+    float4 az[kStreamParts];
+#pragma unroll
+    for (int k = 0; k < kStreamParts; ++k)
+      if (k < nz) {
+        mz[k] = base[k * REC + g];
+        lz[k] = base[k * REC + 16 + g];
+        az[k] = *reinterpret_cast<const float4*>(base + k * REC + 32 + g * D + col);
+      }
+    float mm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kStreamParts; ++k)
+      if (k < nz) mm = fmaxf(mm, mz[k]);
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    float ls = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kStreamParts; ++k)
+      if (k < nz) {
+        const float w = mz[k] == -INFINITY ? 0.0f : fast_exp2(mz[k] - mm);
+        s.x = fmaf(w, az[k].x, s.x);
+        s.y = fmaf(w, az[k].y, s.y);
+        s.z = fmaf(w, az[k].z, s.z);
+        s.w = fmaf(w, az[k].w, s.w);
+        ls = fmaf(w, lz[k], ls);
+      }
+    const float inv = ls > 0.0f ? 1.0f / ls : 0.0f;
+    S* o = reinterpret_cast<S*>(a.out) + static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + g) * a.out_sh +
+           col;
+    o[0] = from_f32<DT>(s.x * inv);
+    o[1] = from_f32<DT>(s.y * inv);
+    o[2] = from_f32<DT>(s.z * inv);
+    o[3] = from_f32<DT>(s.w * inv);
   }
 }
 
@@ -1141,7 +1253,8 @@ using StreamFn = void (*)(StreamArgs);
 
 struct StreamPick {
   StreamFn main[2][2] = {};   // [fused: with the step's K/V append][planned: from a work plan]
-  StreamFn merge[2][2][2] = {};  // [fused][planned][2 streams: a few long segments]
+  StreamFn merge[2][2][2] = {};  // [fused][planned][2 streams and runs: a few long segments]
+  StreamFn fold[2] = {};         // [planned]
   int ring_bytes = 0;  // per wavefront
 };
 
@@ -1157,10 +1270,12 @@ StreamPick pick_one() {
   p.merge[0][1][0] = paged_decode_stream_merge<DT, D, false, true, 1>;
   p.merge[1][0][0] = paged_decode_stream_merge<DT, D, true, false, 1>;
   p.merge[1][1][0] = paged_decode_stream_merge<DT, D, true, true, 1>;
-  p.merge[0][0][1] = paged_decode_stream_merge<DT, D, false, false, 2>;
-  p.merge[0][1][1] = paged_decode_stream_merge<DT, D, false, true, 2>;
-  p.merge[1][0][1] = paged_decode_stream_merge<DT, D, true, false, 2>;
-  p.merge[1][1][1] = paged_decode_stream_merge<DT, D, true, true, 2>;
+  p.merge[0][0][1] = paged_decode_stream_merge<DT, D, false, false, kWideMergeStreams>;
+  p.merge[0][1][1] = paged_decode_stream_merge<DT, D, false, true, kWideMergeStreams>;
+  p.merge[1][0][1] = paged_decode_stream_merge<DT, D, true, false, kWideMergeStreams>;
+  p.merge[1][1][1] = paged_decode_stream_merge<DT, D, true, true, kWideMergeStreams>;
+  p.fold[0] = paged_decode_stream_fold<DT, D, false>;
+  p.fold[1] = paged_decode_stream_fold<DT, D, true>;
   p.ring_bytes = NS * Ring<D, QR>::STAGE;
   return p;
 }
@@ -1185,27 +1300,39 @@ int stream_min_tiles() {
   return 4;
 }
 
-// Calls with at most this many segments (batch x kv heads) merge with 2 streams per
-// workgroup: a few long sequences, whose segments are split into tens of pieces each
-// (B=1 at 32k keys: 29.2 -> 26.4 us per call, B=4 at 8k: 18.2 -> 15.1 us, B=16 at 16k:
-// 37.1 -> 34.2 us). Batches of more segments have a handful of pieces per segment.
+// Calls with at most kWideMergeSegments segments (batch x kv heads) merge with 2 streams per
+// workgroup: a few long sequences, whose segments are split into tens of pieces each (B=1 at
+// 32k keys: 29.2 -> 26.4 us per call, B=4 at 8k: 18.2 -> 15.1 us, B=16 at 16k: 37.1 -> 34.2
+// us). Calls with at most kPartsSegments segments also cut a segment of more than one round of
+// chunks into kStreamParts runs, one workgroup each, folded by a second kernel, and allow 256
+// pieces per segment (B=1 at 32k: 26.4 -> 18.2 us; B=2 at 32k, 28q/4kv d128: 39.8 -> 37.6
+// us); with 16 to 64 segments the fold's launch costs more than it saves (B=16 at 16k: 34.0
+// -> 39.5 us). Batches of more segments have a handful of pieces per segment.
 constexpr int64_t kWideMergeSegments = 64;
+constexpr int64_t kPartsSegments = 16;
 int stream_wide_merge(int64_t segments) { return segments <= kWideMergeSegments ? 1 : 0; }
+int stream_merge_parts(int64_t segments) { return segments <= kPartsSegments ? kStreamParts : 1; }
 
-// Most pieces per segment on average (see stream_active_waves). 64 measured best for one to
-// four long sequences, with either merge (one-stream merge, B=1 at 32k keys: 74 -> 32 us per
-// call; 128: 31 us, 256: 42 us, 32: 46 us; two-stream merge: 26.4 us, 128: 23.3 us but B=4
-// at 8k 18.6 against 15.1 us, 256: 29.7 us) and leaves batches of hundreds of sequences
-// untouched.
-int stream_max_pieces() {
+// Most pieces per segment on average (see stream_active_waves). With the one- or two-stream
+// merge, 64 measured best for one to four long sequences (one-stream merge, B=1 at 32k keys:
+// 74 -> 32 us per call; 128: 31 us, 256: 42 us, 32: 46 us; two-stream merge: 26.4 us, 128:
+// 23.3 us but B=4 at 8k 18.6 against 15.1 us) and leaves batches of hundreds of sequences
+// untouched; with merge runs, 256 (B=1 at 32k: 18.2 us, 64: 29.2 us, 1024: 18.5 us).
+int stream_max_pieces(int64_t segments) {
   if (const char* env = std::getenv("MIP_STREAM_MAX_PIECES")) {
     const int v = std::atoi(env);
     if (v > 0) return v;
   }
-  return MIP_STREAM_MAX_PIECES;
+  return stream_merge_parts(segments) > 1 ? 256 : MIP_STREAM_MAX_PIECES;
 }
 
 }  // namespace
+
+int64_t stream_part_floats(const StreamConfig& cfg, int batch, int num_kv_heads) {
+  const int64_t segments = static_cast<int64_t>(batch) * num_kv_heads;
+  const int parts = stream_merge_parts(segments);
+  return parts > 1 ? segments * parts * cfg.rec_floats : 0;
+}
 
 StreamConfig stream_config(int dtype, int d, int group, int batch) {
   StreamConfig c{};
@@ -1234,13 +1361,16 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, i
   StreamArgs sa = sa_in;
   sa.tw = cfg.tw;
   sa.min_tiles = stream_min_tiles();
-  sa.max_pieces = stream_max_pieces();
+  sa.max_pieces = stream_max_pieces(static_cast<int64_t>(batch) * num_kv_heads);
   sa.rec_stride = static_cast<int>(cfg.rec_floats);
   const int fused = sa.app.slots != nullptr, planned = sa.plan != nullptr;
   hipLaunchKernelGGL(p.main[fused][planned], dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
-  const int wide = stream_wide_merge(static_cast<int64_t>(batch) * num_kv_heads);
-  hipLaunchKernelGGL(p.merge[fused][planned][wide], dim3(num_kv_heads, batch), dim3(wide ? 512 : 256), 0, stream,
-                     sa);
+  const int64_t segments = static_cast<int64_t>(batch) * num_kv_heads;
+  const int wide = stream_wide_merge(segments);
+  sa.parts = stream_merge_parts(segments);
+  hipLaunchKernelGGL(p.merge[fused][planned][wide], dim3(num_kv_heads, batch, sa.parts),
+                     dim3(wide ? 256 * kWideMergeStreams : 256), 0, stream, sa);
+  if (sa.parts > 1) hipLaunchKernelGGL(p.fold[planned], dim3(num_kv_heads, batch), dim3(256), 0, stream, sa);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -1257,7 +1387,8 @@ PlanLayout plan_layout(const StreamConfig& cfg, int batch, int num_kv_heads, int
   // ceil(max_tiles / (segments * max_pieces)) when the piece cap sets W.
   const int64_t min_tiles = stream_min_tiles();
   const int64_t per_wave = (max_tiles + cfg.tw - 1) / cfg.tw;
-  const int64_t seg_cap = static_cast<int64_t>(batch) * num_kv_heads * stream_max_pieces();
+  const int64_t segments = static_cast<int64_t>(batch) * num_kv_heads;
+  const int64_t seg_cap = segments * stream_max_pieces(segments);
   const int64_t per_piece = (max_tiles + seg_cap - 1) / seg_cap;
   l.wave_cap = per_wave > min_tiles ? per_wave : min_tiles;
   if (per_piece > l.wave_cap) l.wave_cap = per_piece;
@@ -1302,7 +1433,7 @@ int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32
   p.cap = max_blocks * block_size;
   p.tw = cfg.tw;
   p.min_tiles = stream_min_tiles();
-  p.max_pieces = stream_max_pieces();
+  p.max_pieces = stream_max_pieces(static_cast<int64_t>(batch) * num_kv_heads);
   p.seg_off = static_cast<int>(l.seg_off);
   p.tile_off = static_cast<int>(l.tile_off);
   p.wave_cap = static_cast<int>(l.wave_cap);

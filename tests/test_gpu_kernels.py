@@ -387,11 +387,13 @@ def test_paged_decode_edge_batches(gpu):
     assert attention_error(values(out), want, "float16") <= TOL["float16"]
 
 
-@pytest.mark.parametrize("batch", [32, 33, 40])
+@pytest.mark.parametrize("batch", [1, 8, 32, 33, 40])
 def test_paged_decode_merge_streams(gpu, batch):
-    """One long sequence among short ones: its segments split into many pieces. At batch 32
-    (64 segments) the merge runs two streams per workgroup, at 33 and 40 one; both against
-    float64, and the planned call bit-identical to the one deriving its split in-kernel."""
+    """One long sequence among short ones: its segments split into many pieces. At batch 1
+    and 8 (2 and 16 segments) the merge cuts a long segment into runs folded by a second
+    kernel, at 32 (64 segments) it runs two streams per workgroup, at 33 and 40 one; all
+    against float64, and the planned call bit-identical to the one deriving its split
+    in-kernel."""
     from engine import paged_ops
 
     announce(f"paged_decode merge streams B={batch}")
