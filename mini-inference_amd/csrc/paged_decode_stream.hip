@@ -845,7 +845,9 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
   const int64_t REC = sa.rec_stride;
   const DecodeArgs& a = sa.a;
   const int kvh = blockIdx.x, b = blockIdx.y, G = sa.group;
-  const int z = blockIdx.z, Z = gridDim.z;  // run z of Z of a parted segment
+  // Run z of Z of a parted segment (only the two-stream merge is launched with Z > 1; with one
+  // stream the run logic folds away at compile time).
+  const int z = NSTR > 1 ? static_cast<int>(blockIdx.z) : 0, Z = NSTR > 1 ? static_cast<int>(gridDim.z) : 1;
   S* out_base = reinterpret_cast<S*>(a.out);
   const int cap = a.max_blocks * a.bs;
   // Fused append: copy sequence b's new K and V rows of this kv head into the pool. The
@@ -927,8 +929,8 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
   constexpr int Q = D / 4;  // column quads per row
   __shared__ float s_m[NSTR][kRC][16];
   __shared__ float s_l[NSTR][kRC][16];
-  const int str = static_cast<int>(threadIdx.x) / 256;
-  const int t = threadIdx.x % 256, tg = t & 15, tr = t >> 4;
+  const int str = NSTR > 1 ? static_cast<int>(threadIdx.x) / 256 : 0;
+  const int t = NSTR > 1 ? static_cast<int>(threadIdx.x) % 256 : static_cast<int>(threadIdx.x), tg = t & 15, tr = t >> 4;
   const int nq = G * Q;  // quads per (kv head, sequence): at most 512
   const int nj = nq > 256 ? 2 : 1;
   float4 acc[2];
@@ -966,7 +968,7 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int qd = t + 256 * j;
-      if (nr > 0 && j < nj && qd < nq) {
+      if ((NSTR == 1 || nr > 0) && j < nj && qd < nq) {
         const int g = qd / Q;
         float cm = mrun[j];
         for (int k = 0; k < nr; ++k) cm = fmaxf(cm, s_m[str][k][g]);
