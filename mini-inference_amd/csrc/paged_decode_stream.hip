@@ -832,13 +832,15 @@ constexpr int kMergeChunk = 16;
 constexpr int kWideMergeStreams = 2;
 constexpr int kStreamParts = 16;
 
-// Combine the pieces of every segment the stream kernel split. Grid (kv heads, batch),
+// Combine the pieces of every segment the stream kernel split. Grid (kv heads, batch, runs),
 // NSTR * 256 threads: NSTR streams of 256 threads take alternate chunks of 16 pieces (each
 // stream with its own online maximum), and stream 0 then combines the streams' states in
 // stream order. NSTR = 1 serves batches of many segments (each segment has few pieces);
 // NSTR = 2 serves a few long sequences, whose segments have up to a few hundred pieces (two
 // streams keep a chunk's 16 partial sums per thread in registers: at 1024 threads a thread
-// has 128 registers, and the chunk buffer alone takes 128).
+// has 128 registers, and the chunk buffer alone takes 128). With runs > 1 (at most 16
+// segments), a segment of more than NSTR chunks is cut into runs of consecutive pieces, one
+// workgroup each, whose states paged_decode_stream_fold combines.
 template <int DT, int D, bool FUSED, bool PLANNED, int NSTR>
 __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamArgs sa) {
   using S = typename Elem<DT>::S;
