@@ -164,23 +164,21 @@ def decode_step(batch, dev, calls_per_step: int | None = None):
     return hot_step, (qs, ks, vs)
 
 
-def long_context_measure(dev, steps: int = 10, layers: int = 4) -> dict:
-    """Append + decode attention at the long-context shape: 28 query / 4 KV heads, head_dim
-    128, bf16, batch 128, contexts log-uniform in [512, 8192], block size 32, the pool churned
-    by 5,000 alloc/free events. A step is the plan plus 28 fused calls (one per layer of the
-    model), cycling over ``layers`` distinct layers of the pool (every layer's work is the
-    same; 4 layers keep the K/V the calls read, 3.3 GB, far above the 256 MB last-level
-    cache). HIP events; the figure is the step time over 28."""
-    import dataclasses
-
+def long_context_measure(dev, steps: int = 10) -> dict:
+    """Append + decode attention at the long-context shape as configured: 28 query / 4 KV heads,
+    head_dim 128, bf16, 28 layers, batch 128, contexts log-uniform in [512, 8192], block size
+    32, block tables randomly permuted over a pool of about 60 % of the 288 GB HBM (every
+    layer's K and V). A step is the plan plus one fused call per layer, each on its own layer
+    of the pool. HIP events; the figure is the step time over 28."""
     import torch
 
     from engine import workloads
 
-    shape = dataclasses.replace(workloads.SHAPES[5], num_layers=layers)
+    shape = workloads.SHAPES[5]
     batch = workloads.build_decode_batch(shape, dev, seed=0)
-    n_calls = workloads.SHAPES[5].num_layers
-    step, _ = decode_step(batch, dev, calls_per_step=n_calls)
+    pool_gb = 2 * batch.cache.k.numel() * batch.cache.k.element_size() / 1e9
+    n_calls = shape.num_layers
+    step, _ = decode_step(batch, dev)
     for _ in range(2):
         step()
     torch.cuda.synchronize()
@@ -188,12 +186,13 @@ def long_context_measure(dev, steps: int = 10, layers: int = 4) -> dict:
     lens = [n + 1 for n in batch.ctx]
     nbytes = attention_bytes(lens, shape) + append_bytes(shape)
     gbps = nbytes / t / 1e9
+    num_blocks = batch.cache.num_blocks
     del batch, step
     torch.cuda.empty_cache()
     return {
         "workload": "paged decode step (KV append + paged attention), 28q/4kv heads d128, bf16, B=128, ctx "
-                    f"log-uniform[512,8192], block 32, churned pool; plan + 28 calls per step over {layers} "
-                    "distinct layers",
+                    f"log-uniform[512,8192], block 32, tables randomly permuted over a {num_blocks}-block pool "
+                    f"({pool_gb:.1f} GB of K/V over 28 layers); plan + 28 calls per step, one per layer",
         "kernel": "paged_decode_stream_tiles<bf16, D=128, QR=8, NS=3> (planned, with the fused append) + "
                   "paged_decode_stream_merge<bf16, D=128>",
         "us_per_layer": round(t * 1e6, 2),
@@ -284,9 +283,8 @@ def prefill_measure(dev, iters: int = 30) -> dict:
     out = torch.empty_like(q)
     k_layer, v_layer = pb.cache.k[0], pb.cache.v[0]
 
-    def call():
-        paged_ops.paged_prefill(q, k_layer, v_layer, ctx.block_tables, ctx.cu_q, ctx.ctx_start, ctx.max_q_len,
-                                out=out)
+    call = paged_ops.prepare_paged_prefill(q, k_layer, v_layer, ctx.block_tables, ctx.cu_q, ctx.ctx_start,
+                                           ctx.max_q_len, out=out)[0]
 
     for _ in range(3):
         call()
@@ -380,10 +378,11 @@ def copy_measure(dev, iters: int = 40, sets: int = 8) -> dict:
     random.Random(5).shuffle(ids)
     sets_t = [torch.tensor([[ids[2 * (i * pairs_per + j)], ids[2 * (i * pairs_per + j) + 1]] for j in range(pairs_per)],
                            dtype=torch.int64, device=dev) for i in range(sets)]
+    calls = [paged_ops.prepare_copy_blocks(k, v, t) for t in sets_t]
     it = [0]
 
     def call():
-        paged_ops.copy_blocks(k, v, sets_t[it[0] % sets])
+        calls[it[0] % sets]()
         it[0] += 1
 
     for _ in range(sets):
@@ -406,6 +405,78 @@ def copy_measure(dev, iters: int = 40, sets: int = 8) -> dict:
     }
 
 
+def hbm_ceiling(dev, nbytes: int, chunk: int = 2048, sets: int = 24, iters: int = 48,
+                grids: tuple[int, ...] = (1024, 2048, 4096, 8192)) -> dict:
+    """What this GPU streams for ``nbytes`` (one decode call's algorithmic bytes): the library's
+    read probe (``mip_hbm_read_probe``) over randomly placed ``chunk``-byte chunks of a 4 GiB
+    buffer, as the paged pool is read, and over one contiguous run, cycling ``sets`` disjoint
+    chunk sets so nothing is served from the 256 MB last-level cache; the fastest of ``grids``
+    (workgroups of 256 threads) is reported. HIP events."""
+    import torch
+
+    from engine import _native
+
+    lib = _native.load()
+    pool_bytes = 4 << 30
+    buf = torch.zeros(pool_bytes // 4, dtype=torch.int32, device=dev)
+    total = pool_bytes // chunk
+    per = nbytes // chunk
+    gen = torch.Generator(device=dev).manual_seed(1)
+    ids = torch.randperm(total, generator=gen, device=dev)[:per * sets].to(torch.int32).view(sets, per).contiguous()
+    seq = [torch.arange(i * per, (i + 1) * per, dtype=torch.int32, device=dev) for i in range(sets)]
+    sink = torch.empty(max(grids) * 256, dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+    for name, chunks in (("random_chunks", [ids[i] for i in range(sets)]), ("sequential", seq)):
+        by_grid = {}
+        for grid in grids:
+            args = [(buf.data_ptr(), pool_bytes, c.data_ptr(), per, chunk, sink.data_ptr(), grid, st) for c in chunks]
+            it = [0]
+
+            def call():
+                a = args[it[0] % sets]
+                it[0] += 1
+                rc = lib.mip_hbm_read_probe(*a)
+                if rc:
+                    _native.check(rc, "mip_hbm_read_probe")
+
+            for _ in range(sets):
+                call()
+            torch.cuda.synchronize()
+            by_grid[grid] = time_loop(call, iters)
+        grid, t = min(by_grid.items(), key=lambda kv: kv[1])
+        out[name] = {"us": round(t * 1e6, 2), "GBps": round(per * chunk / t / 1e9, 1),
+                     "frac": round(per * chunk / t / 1e9 / HBM_PEAK_GBPS, 4), "grid": grid,
+                     "us_by_grid": {str(g): round(v * 1e6, 2) for g, v in by_grid.items()}}
+    del buf, ids, seq, sink
+    torch.cuda.empty_cache()
+    out.update({"kernel": "hbm_read_probe_kernel", "bytes": per * chunk, "chunk_bytes": chunk,
+                "workload": f"read {per * chunk} B as {per} randomly placed {chunk}-byte chunks of a 4 GiB buffer "
+                            f"(and as one contiguous run), {sets} disjoint sets cycled, the fastest of grids "
+                            f"{list(grids)} x 256 threads"})
+    return out
+
+
+def small_batch_decode(dev, steps: int, warmup: int) -> dict:
+    """Full decode step at the 32-sequence fp16 shape: random-init Qwen2.5-0.5B, 24 layers,
+    contexts U[128, 1024], block 16, tables randomly permuted over a 16,384-block pool; graphed
+    and eager, as decode_tok_s."""
+    import torch
+
+    from engine import workloads
+
+    batch = workloads.build_decode_batch(workloads.SHAPES[2], dev, seed=0)
+    dm = decode_tok_s(batch, steps=steps, warmup=warmup)
+    del batch
+    torch.cuda.empty_cache()
+    return {
+        "workload": "full decode step, random-init Qwen2.5-0.5B, fp16, B=32, ctx U[128,1024], block 16, "
+                    "tables permuted over 16384 blocks",
+        "tok_s": round(dm["tok_s"], 1), "ms_per_step": round(dm["ms_per_step"], 3),
+        "eager_tok_s": round(dm["eager_tok_s"], 1), "eager_ms_per_step": round(dm["eager_ms_per_step"], 3),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -420,7 +491,14 @@ def main() -> int:
                     help="skip the long-context decode measurement (28q/4kv heads d128, B=128, ctx up to 8192)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 512 MiB device copy three times (HBM counter scale for rocprofv3 --pmc)")
+    ap.add_argument("--decode-algo", choices=("auto", "stream", "mfma", "valu"), default="auto",
+                    help="force the decode attention kernel (kernel comparison; the headline uses auto = stream)")
+    ap.add_argument("--no-probe", action="store_true", help="skip the HBM read-probe ceiling")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the headline decode call (no model, prefill, long-context, probe or CPU legs)")
     args = ap.parse_args()
+    if args.headline_only:
+        args.no_model = args.no_prefill = args.no_long_context = args.no_probe = args.no_cpu_baseline = True
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -436,6 +514,10 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda", 0)
+    if args.decode_algo != "auto":
+        from engine import _native
+
+        _native.set_decode_algo(args.decode_algo)
     if args.copy_calibration:
         src = torch.empty(256 << 20, dtype=torch.bfloat16, device=dev)  # 512 MiB
         dst = torch.empty_like(src)
@@ -509,6 +591,23 @@ def main() -> int:
         },
     }
 
+    if args.decode_algo != "auto":
+        result["decode_algo"] = args.decode_algo
+        result["roofline"]["kernel"] = f"forced decode algorithm: {args.decode_algo}"
+
+    if not args.no_probe:
+        try:
+            hc = hbm_ceiling(dev, a_bytes + p_bytes)
+            hc["decode_call_frac_of_random_chunks"] = round(achieved / hc["random_chunks"]["GBps"], 4)
+            result["hbm_ceiling"] = hc
+            log(f"hbm probe: {hc['bytes']} B as random 2 KiB chunks {hc['random_chunks']['us']} us "
+                f"({hc['random_chunks']['GBps']} GB/s), sequential {hc['sequential']['us']} us "
+                f"({hc['sequential']['GBps']} GB/s); the decode call reaches "
+                f"{hc['decode_call_frac_of_random_chunks']:.1%} of the random-chunk rate")
+        except Exception as exc:
+            log(f"hbm probe failed: {exc!r}")
+            result["hbm_ceiling"] = None
+
     if not args.no_model:
         try:
             dm = decode_tok_s(batch, steps=max(10, min(args.steps, 30)), warmup=3)
@@ -520,6 +619,14 @@ def main() -> int:
         except Exception as exc:  # the headline kernel numbers stand on their own
             log(f"full-model decode failed: {exc!r}")
             result["decode_tok_s"] = None
+        try:
+            sb = small_batch_decode(dev, steps=max(10, min(args.steps, 30)), warmup=3)
+            result["small_batch_decode"] = sb
+            log(f"full-model decode B=32 fp16: graph {sb['ms_per_step']} ms/step ({sb['tok_s']} tok/s), "
+                f"eager {sb['eager_ms_per_step']} ms/step ({sb['eager_tok_s']} tok/s)")
+        except Exception as exc:
+            log(f"B=32 full-model decode failed: {exc!r}")
+            result["small_batch_decode"] = None
 
     if not args.no_prefill:
         try:

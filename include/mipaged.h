@@ -50,6 +50,19 @@ enum mip_status { MIP_OK = 0, MIP_EINVAL = -22, MIP_EUNSUPPORTED = -95 };
 /* Library version, (major << 16) | minor. */
 int mip_version(void);
 
+/*
+ * Decode attention algorithm (no reference counterpart: the reference has one path, SDPA).
+ * MIP_ALGO_AUTO picks per shape: the stream-K MFMA kernel for 16-bit K/V at head_dim 64/128
+ * (batch <= 4096), else the per-partition MFMA kernel, else the VALU kernel (fp32, other head
+ * sizes). A forced algorithm applies only where its kernel exists for the shape. The setting is
+ * process-wide, starts from the MIP_DECODE_ALGO environment variable (valu | mfma | stream,
+ * read once), and is meant for kernel comparisons and tests; it must not change while decode
+ * calls are being enqueued, since the workspace and plan sizes depend on it. Returns the
+ * previous setting, or MIP_EINVAL for an unknown value.
+ */
+enum mip_decode_algo { MIP_ALGO_AUTO = 0, MIP_ALGO_VALU = 1, MIP_ALGO_MFMA = 2, MIP_ALGO_STREAM = 3 };
+int mip_set_decode_algo(int32_t algo);
+
 /* Human-readable text for a status code returned by any entry point. */
 const char* mip_status_string(int status);
 
@@ -144,7 +157,10 @@ int mip_rope_kv_append(void* q, int64_t q_stride_tok, int64_t q_stride_head,
  * walking the block tables (every layer of a decode step shares one plan). `plan_bytes` is
  * the size of the plan buffer: below mip_paged_decode_plan_bytes for this shape it is
  * MIP_EINVAL. The plan is ignored where the stream kernel does not run and for
- * block_size < 16.
+ * block_size < 16. A plan made for another batch size or kv-head count (its header does not
+ * match the call) cannot be detected before launch, since it lives in device memory: the call
+ * then writes NaN to every output row and, for mip_paged_decode_append, leaves the pool
+ * unchanged.
  */
 int mip_paged_decode(void* out, int64_t out_stride_b, int64_t out_stride_h,
                      const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -200,8 +216,8 @@ int mip_paged_decode_append(const void* k_new, const void* v_new,
  * launched) for shapes the stream kernel does not run and for block_size < 16 (a tile must
  * lie in one block); mip_paged_decode_plan_bytes returns 0 for those. The plan buffer must
  * be 8-byte aligned; it holds int32 data and stays valid while context_lens, block_tables
- * and the shape do not change. A plan made for another batch size or kv-head count is
- * ignored by the decode kernel (nothing is computed).
+ * and the shape do not change. A decode call given a plan made for another batch size or
+ * kv-head count writes NaN outputs and appends nothing (see mip_paged_decode).
  */
 size_t mip_paged_decode_plan_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_dim, int32_t block_size,
@@ -232,8 +248,13 @@ int mip_paged_decode_plan(const int32_t* context_lens, const int32_t* block_tabl
  * pool (append first). Products and sums in fp32, output rounded once to dtype. Keys past
  * max_blocks_per_seq * block_size are never read (positions beyond are clamped to the last
  * one). max_q_len must be >= every cu_q[s + 1] - cu_q[s]; it only sizes the grid, which
- * depends on the integer arguments alone. Supported: 16-bit dtypes, head_dim 64 or 128,
- * group <= 16 (else MIP_EUNSUPPORTED); q rows 16-byte aligned, out rows 8-byte aligned.
+ * depends on the integer arguments alone.
+ *
+ * Kernels: 16-bit dtypes at head_dim 64 or 128 with group <= 16 run the MFMA prefill kernel
+ * (q rows 16-byte aligned, out rows 8-byte aligned). Every other shape with group <= 8 and
+ * head_dim a power of two in 8 .. 256 (fp32 included) runs the VALU decode kernel, one
+ * workgroup per (new token, kv head) over that token's keys (q rows 4-byte aligned); the
+ * grid then has num_seqs * max_q_len workgroups per kv head. Other shapes: MIP_EUNSUPPORTED.
  */
 int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_stride_head,
                       const void* q, int64_t q_stride_tok, int64_t q_stride_head,

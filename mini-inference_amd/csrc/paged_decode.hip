@@ -30,9 +30,10 @@
 //   * Softmax is online in base 2 with a wave-uniform running max per head that is only
 //     raised when some key exceeds it by more than kRescaleLog2 (then the partial sums are
 //     rescaled), so most passes need no cross-lane max.
+#include <atomic>
+#include <cmath>
 #include <cstdlib>
 #include <type_traits>
-#include <cmath>
 
 #include "paged_decode_common.h"
 
@@ -151,12 +152,28 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_part(DecodeArgs a) {
   __shared__ float sh_l[kNW][G];
   __shared__ float sh_acc[kNW][G][D];
 
-  const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int kvh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int h0 = kvh * G;
 
-  int ctx = a.lens[b];
+  // Decode: (partition, kv head, sequence). Packed prefill: (sequence x new token, kv head),
+  // one partition; the row's keys are its sequence's keys up to its own position.
+  int part, b, ctx, trow;
+  if (a.cu_q) {
+    const int x = blockIdx.x, s = x / a.max_q_len, i = x - s * a.max_q_len;
+    const int r0 = a.cu_q[s];
+    if (r0 + i >= a.cu_q[s + 1]) return;
+    part = 0;
+    b = r0 + i;
+    trow = s;
+    ctx = a.ctx_start[s] + i + 1;
+  } else {
+    part = blockIdx.x;
+    b = blockIdx.z;
+    trow = b;
+    ctx = a.lens[b];
+  }
   const int cap = a.max_blocks * a.bs;
   ctx = ctx < cap ? ctx : cap;
   const int np_b = ctx > 0 ? (ctx + a.part_tokens - 1) / a.part_tokens : 1;
@@ -195,7 +212,7 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_part(DecodeArgs a) {
     for (int e = 0; e < VEPL; ++e) acc[g][e] = 0.0f;
   }
 
-  const int32_t* table = a.bt + static_cast<int64_t>(b) * a.bt_stride;
+  const int32_t* table = a.bt + static_cast<int64_t>(trow) * a.bt_stride;
   const int ts = lane / LPT, u = lane % LPT;
 
   auto compute = [&](const Frag& f) {
@@ -650,19 +667,29 @@ bool mfma_eligible(int dtype, int d, int g) {
   return (dtype == MIP_BF16 || dtype == MIP_F16) && (d == 64 || d == 128) && g >= 1 && g <= 16;
 }
 
+// Forced algorithm (mip_set_decode_algo; MIP_ALGO_AUTO = the default choice below). Its
+// first value comes from MIP_DECODE_ALGO=valu|mfma|stream, read once.
+int algo_from_env() {
+  const char* env = std::getenv("MIP_DECODE_ALGO");
+  const char f = env ? env[0] : 0;
+  return f == 'v' ? MIP_ALGO_VALU : f == 'm' ? MIP_ALGO_MFMA : f == 's' ? MIP_ALGO_STREAM : MIP_ALGO_AUTO;
+}
+std::atomic<int>& forced_algo() {
+  static std::atomic<int> v{algo_from_env()};
+  return v;
+}
+
 // Default: the stream-K MFMA kernel for 16-bit data at head_dim 64/128 (balanced persistent
 // work split, the fastest under rocprof at the Qwen shapes) while its per-sequence scan fits
 // in LDS (batch <= 4096); otherwise the per-partition MFMA kernel; the VALU kernel for fp32
-// and the other head sizes.
-// MIP_DECODE_ALGO=valu|mfma|stream forces one where it applies (kernel comparison).
+// and the other head sizes. A forced algorithm applies where its kernel exists.
 Algo choose_algo(int dtype, int d, int g, int batch) {
-  const char* env = std::getenv("MIP_DECODE_ALGO");
-  const char f = env ? env[0] : 0;
+  const int f = forced_algo().load(std::memory_order_relaxed);
   const bool mfma_ok = mfma_eligible(dtype, d, g);
   const bool stream_ok = mfma_ok && stream_config(dtype, d, g, batch).ok;
-  if (f == 'v' && g <= 8) return Algo::kValu;
-  if (f == 'm' && mfma_ok) return Algo::kMfma;
-  if (f == 's' && stream_ok) return Algo::kStream;
+  if (f == MIP_ALGO_VALU && g <= 8) return Algo::kValu;
+  if (f == MIP_ALGO_MFMA && mfma_ok) return Algo::kMfma;
+  if (f == MIP_ALGO_STREAM && stream_ok) return Algo::kStream;
   return stream_ok ? Algo::kStream : mfma_ok ? Algo::kMfma : Algo::kValu;
 }
 
@@ -673,14 +700,19 @@ int pass_tokens(Algo algo, int dtype, int d) {
   return kWave / (d / ch);
 }
 
+// Keys per partition of the partition kernels (MIP_PART_TOKENS, read once).
+int part_tokens_env() {
+  static const int v = [] {
+    const char* env = std::getenv("MIP_PART_TOKENS");
+    const int x = env ? std::atoi(env) : 0;
+    return x > 0 ? x : kDefaultPartTokens;
+  }();
+  return v;
+}
+
 int part_tokens_for(Algo algo, int dtype, int d) {
   const int align = kNW * pass_tokens(algo, dtype, d);
-  int want = kDefaultPartTokens;
-  if (const char* env = std::getenv("MIP_PART_TOKENS")) {
-    const int v = std::atoi(env);
-    if (v > 0) want = v;
-  }
-  return static_cast<int>(align_up(want, align));
+  return static_cast<int>(align_up(part_tokens_env(), align));
 }
 
 struct WsLayout {
@@ -812,9 +844,70 @@ KernelPair pick_kernel(Algo algo, int dtype, int d, int g) {
 }
 
 }  // namespace
+
+namespace decode {
+
+int valu_prefill_launch(void* out, int64_t out_stride_tok, int64_t out_stride_head, const void* q,
+                        int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache, const void* v_cache,
+                        int64_t num_cache_blocks, const int32_t* block_tables, int64_t bt_stride, const int32_t* cu_q,
+                        const int32_t* ctx_start, int32_t num_seqs, int32_t max_q_len, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
+                        float scale, int32_t dtype, hipStream_t stream) {
+  const int group = num_heads / num_kv_heads;
+  if (group > 8) return MIP_EUNSUPPORTED;
+  const KernelPair kp = pick_kernel(Algo::kValu, dtype, head_dim, group);
+  if (!kp.part) return MIP_EUNSUPPORTED;
+  const int64_t es = dtype == MIP_F32 ? 4 : 2;
+  if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return MIP_EINVAL;
+  // q is read 4 bytes at a time, outputs are written one element at a time.
+  if ((reinterpret_cast<uintptr_t>(q) | static_cast<uint64_t>(q_stride_tok * es) |
+       static_cast<uint64_t>(q_stride_head * es)) & 3)
+    return MIP_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(out) | static_cast<uint64_t>(out_stride_tok * es) |
+       static_cast<uint64_t>(out_stride_head * es)) & (es - 1))
+    return MIP_EINVAL;
+  const int64_t cap = static_cast<int64_t>(max_blocks_per_seq) * block_size;
+  if (cap >= (int64_t{1} << 30)) return MIP_EINVAL;
+  if (num_cache_blocks * num_kv_heads * block_size >= (int64_t{1} << 31)) return MIP_EINVAL;
+  const int64_t grid_x = static_cast<int64_t>(num_seqs) * max_q_len;
+  if (grid_x >= (int64_t{1} << 31) || num_kv_heads > 65535) return MIP_EUNSUPPORTED;
+  DecodeArgs a{};
+  a.out = static_cast<char*>(out);
+  a.out_sb = out_stride_tok;
+  a.out_sh = out_stride_head;
+  a.q = static_cast<const char*>(q);
+  a.q_sb = q_stride_tok;
+  a.q_sh = q_stride_head;
+  a.k = static_cast<const char*>(k_cache);
+  a.v = static_cast<const char*>(v_cache);
+  a.ncb = num_cache_blocks;
+  a.bt = block_tables;
+  a.bt_stride = bt_stride;
+  a.hq = num_heads;
+  a.hkv = num_kv_heads;
+  a.bs = block_size;
+  a.log2_bs = ilog2_exact(block_size);
+  a.max_blocks = max_blocks_per_seq;
+  // One partition covers the longest row (at most max_blocks_per_seq * block_size keys).
+  a.part_tokens = static_cast<int>(align_up(cap, kNW * pass_tokens(Algo::kValu, dtype, head_dim)));
+  a.nparts = 1;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.cu_q = cu_q;
+  a.ctx_start = ctx_start;
+  a.max_q_len = max_q_len;
+  hipLaunchKernelGGL(kp.part, dim3(static_cast<unsigned>(grid_x), num_kv_heads, 1), dim3(kNW * kWave), 0, stream, a);
+  return status_from_hip(hipGetLastError());
+}
+
+}  // namespace decode
 }  // namespace mip
 
 using namespace mip;
+
+extern "C" int mip_set_decode_algo(int32_t algo) {
+  if (algo < MIP_ALGO_AUTO || algo > MIP_ALGO_STREAM) return MIP_EINVAL;
+  return forced_algo().exchange(algo);
+}
 
 extern "C" size_t mip_paged_decode_workspace(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                              int32_t block_size, int32_t max_blocks_per_seq, int32_t dtype) {

@@ -28,6 +28,13 @@ struct DecodeArgs {
   float scale_log2;
   float* ws_acc;  // [B][Hq][nparts][D]
   float* ws_ml;   // [B][Hq][nparts][2]
+  // Packed prefill rows (cu_q != nullptr, VALU kernel only): workgroup x of the grid
+  // (num_seqs * max_q_len, kv heads) is new token i = x % max_q_len of sequence s =
+  // x / max_q_len, packed row cu_q[s] + i (absent past cu_q[s + 1]); it attends keys
+  // 0 .. ctx_start[s] + i through table row s. One partition per row (no merge).
+  const int32_t* cu_q;
+  const int32_t* ctx_start;
+  int max_q_len;
 };
 
 // The step's new K/V rows, appended by the stream kernel itself (mip_paged_decode_append).
@@ -189,6 +196,21 @@ void stream_plan_offsets(const StreamConfig& cfg, int batch, int num_kv_heads, i
                          int32_t* seg_off, int32_t* tile_off, int32_t* wave_cap);
 int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32_t* block_tables, int64_t bt_stride,
                        int batch, int num_kv_heads, int block_size, int max_blocks, int32_t* plan, hipStream_t stream);
+
+// Tuning knobs of the stream split, read from the environment once per process
+// (MIP_STREAM_MIN_TILES, MIP_STREAM_MAX_PIECES; 0 = the built-in choice).
+int stream_min_tiles();
+int stream_max_pieces_env();
+
+// Packed prefill attention on the VALU decode kernel (paged_decode.hip), for the shapes the
+// MFMA prefill kernel does not cover: fp32, head sizes other than 64 / 128 (8 .. 256, powers
+// of two), up to 8 query heads per kv head. Arguments as mip_paged_prefill, checked there.
+int valu_prefill_launch(void* out, int64_t out_stride_tok, int64_t out_stride_head, const void* q,
+                        int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache, const void* v_cache,
+                        int64_t num_cache_blocks, const int32_t* block_tables, int64_t bt_stride, const int32_t* cu_q,
+                        const int32_t* ctx_start, int32_t num_seqs, int32_t max_q_len, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
+                        float scale, int32_t dtype, hipStream_t stream);
 
 }  // namespace decode
 }  // namespace mip

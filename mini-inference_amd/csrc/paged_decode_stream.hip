@@ -36,7 +36,9 @@
 //   twice, V^T against hi and again against lo. Online softmax in base 2 with a per-head running max
 //   that is only raised when a key exceeds it by more than kRescaleLog2.
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "paged_decode_common.h"
 
@@ -854,18 +856,22 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
   const int cap = a.max_blocks * a.bs;
   // Fused append: copy sequence b's new K and V rows of this kv head into the pool. The
   // stream kernel, which ran before this one, took the newest key straight from the source,
-  // so nothing reads these pool rows in this call.
+  // so nothing reads these pool rows in this call. The rows are loaded here and stored once
+  // the plan is known to fit the call.
   const AppendRows& ap = sa.app;
-  if (FUSED && z == 0 && threadIdx.x < 2 * (D * 2 / 16)) {
-    constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
+  constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
+  const bool app_lane = FUSED && z == 0 && threadIdx.x < 2 * CPR;
+  uint4 app_row = make_uint4(0u, 0u, 0u, 0u);
+  char* app_dst = nullptr;
+  if (app_lane) {
     const int side = threadIdx.x / CPR, c = threadIdx.x % CPR;
     const int64_t slot = ap.slots[b];
     if (slot >= 0 && slot < a.ncb * a.bs) {
       const char* src = side ? ap.v + static_cast<int64_t>(b) * ap.v_st + static_cast<int64_t>(kvh) * ap.v_sh
                              : ap.k + static_cast<int64_t>(b) * ap.k_st + static_cast<int64_t>(kvh) * ap.k_sh;
-      char* dst = (side ? ap.v_cache : ap.k_cache) +
-                  (((slot >> a.log2_bs) * a.hkv + kvh) * a.bs + (slot & (a.bs - 1))) * (D * 2);
-      *reinterpret_cast<uint4*>(dst + c * 16) = *reinterpret_cast<const uint4*>(src + c * 16);
+      app_dst = (side ? ap.v_cache : ap.k_cache) +
+                (((slot >> a.log2_bs) * a.hkv + kvh) * a.bs + (slot & (a.bs - 1))) * (D * 2) + c * 16;
+      app_row = *reinterpret_cast<const uint4*>(src + c * 16);
     }
   }
   int L, gw_lo, gw_hi;
@@ -878,12 +884,20 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
     gw_hi = gw_lo + load_uniform_i32(sd + 1) - 1;
     lo_split = load_uniform_i32(sd + 2) != 0;
     L = load_uniform_i32(sd + 3);
-    // The main kernel computed nothing with a plan of another shape; its records stay unread.
-    if (pb != sa.batch || ph != a.hkv || ps != sa.plan_seg_off || gw_lo < 0 || gw_hi >= sa.tw) return;
+    // A plan of another shape: the main kernel computed nothing. The call fails visibly:
+    // NaN in every output row of this segment, and the pool is left as it was (no append).
+    if (pb != sa.batch || ph != a.hkv || ps != sa.plan_seg_off || gw_lo < 0 || gw_hi >= sa.tw) {
+      if (z == 0)
+        for (int i = threadIdx.x; i < G * D; i += blockDim.x)
+          out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + i / D) * a.out_sh + i % D] =
+              from_f32<DT>(__builtin_nanf(""));
+      return;
+    }
   } else {
     L = a.lens[b];
     L = L < cap ? L : cap;
   }
+  if (app_dst) *reinterpret_cast<uint4*>(app_dst) = app_row;
   if (L <= 0) {
     if (z == 0)
       for (int i = threadIdx.x; i < G * D; i += blockDim.x)
@@ -1296,13 +1310,6 @@ StreamPick pick(int dtype, int d, int group) {
   return {};
 }
 
-int stream_min_tiles() {
-  if (const char* env = std::getenv("MIP_STREAM_MIN_TILES")) {
-    const int v = std::atoi(env);
-    if (v > 0) return v;
-  }
-  return 4;
-}
 
 // Calls with at most kWideMergeSegments segments (batch x kv heads) merge with 2 streams per
 // workgroup: a few long sequences, whose segments are split into tens of pieces each (B=1 at
@@ -1323,14 +1330,42 @@ int stream_merge_parts(int64_t segments) { return segments <= kPartsSegments ? k
 // 23.3 us but B=4 at 8k 18.6 against 15.1 us) and leaves batches of hundreds of sequences
 // untouched; with merge runs, 256 (B=1 at 32k: 18.2 us, 64: 29.2 us, 1024: 18.5 us).
 int stream_max_pieces(int64_t segments) {
-  if (const char* env = std::getenv("MIP_STREAM_MAX_PIECES")) {
-    const int v = std::atoi(env);
-    if (v > 0) return v;
-  }
+  const int v = stream_max_pieces_env();
+  if (v > 0) return v;
   return stream_merge_parts(segments) > 1 ? 256 : MIP_STREAM_MAX_PIECES;
 }
 
+int env_positive(const char* name) {
+  const char* env = std::getenv(name);
+  const int v = env ? std::atoi(env) : 0;
+  return v > 0 ? v : 0;
+}
+
+// Occupancy of the stream kernel per (device, dtype, head_dim, q rows): one query per
+// process and shape, since it is the same for every call.
+struct GridKey {
+  int dev, dtype, d, qr;
+  bool operator==(const GridKey& o) const { return dev == o.dev && dtype == o.dtype && d == o.d && qr == o.qr; }
+};
+struct GridEntry {
+  GridKey key;
+  int grid;  // workgroups of the persistent grid (0: the query failed)
+};
+
 }  // namespace
+
+int stream_min_tiles() {
+  static const int v = [] {
+    const int e = env_positive("MIP_STREAM_MIN_TILES");
+    return e > 0 ? e : 4;
+  }();
+  return v;
+}
+
+int stream_max_pieces_env() {
+  static const int v = env_positive("MIP_STREAM_MAX_PIECES");
+  return v;
+}
 
 int64_t stream_part_floats(const StreamConfig& cfg, int batch, int num_kv_heads) {
   const int64_t segments = static_cast<int64_t>(batch) * num_kv_heads;
@@ -1343,16 +1378,38 @@ StreamConfig stream_config(int dtype, int d, int group, int batch) {
   if (batch < 1 || batch > kStreamMaxBatch || group < 1 || group > 16) return c;
   const StreamPick p = pick(dtype, d, group);
   if (!p.main[0][0]) return c;
-  const int scan_bytes = (2 * batch + 1 + kSW) * 4;
+  // The LDS rings (at least 60 KiB per workgroup) always exceed the scan area of
+  // kStreamMaxBatch sequences (33 KiB), so the size, and with it the occupancy, does not
+  // depend on the batch.
+  const int scan_bytes = (2 * kStreamMaxBatch + 1 + kSW) * 4;
   const int ring_bytes = kSW * p.ring_bytes;
+  static_assert((2 * kStreamMaxBatch + 1 + kSW) * 4 <= kSW * 3 * (32 + 8) * 128, "scan area within the rings");
   c.lds_bytes = scan_bytes > ring_bytes ? scan_bytes : ring_bytes;
-  int dev = 0, cus = 0, per_cu = 0;
+  int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return c;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return c;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(p.main[0][0]), kSW * kWave,
-                                                   c.lds_bytes) != hipSuccess)
-    return c;
-  c.grid = cus * (per_cu > 0 ? per_cu : 1);
+  const GridKey key{dev, dtype, d, group <= 8 ? 8 : 16};
+  static std::mutex mu;
+  static std::vector<GridEntry> known;
+  int grid = -1;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (const GridEntry& e : known)
+      if (e.key == key) grid = e.grid;
+  }
+  if (grid < 0) {
+    int cus = 0, per_cu = 0;
+    grid = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0 &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(p.main[0][0]),
+                                                     kSW * kWave, c.lds_bytes) == hipSuccess)
+      grid = cus * (per_cu > 0 ? per_cu : 1);
+    if (grid > 0) {  // a failed query is not remembered: the next call asks again
+      std::lock_guard<std::mutex> lock(mu);
+      known.push_back(GridEntry{key, grid});
+    }
+  }
+  if (grid <= 0) return c;
+  c.grid = grid;
   c.tw = c.grid * kSW;
   c.rec_floats = 32 + static_cast<int64_t>(group) * d;
   c.ok = true;

@@ -561,7 +561,15 @@ extern "C" int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_
   if (num_seqs == 0 || max_q_len == 0) return MIP_OK;
   if (!out || !q || !k_cache || !v_cache || !block_tables || !cu_q || !ctx_start) return MIP_EINVAL;
   const int group = num_heads / num_kv_heads;
-  if (dtype == MIP_F32 || (head_dim != 64 && head_dim != 128) || group > 16) return MIP_EUNSUPPORTED;
+  if (dtype == MIP_F32 || (head_dim != 64 && head_dim != 128) || group > 16) {
+    // Shapes without an MFMA prefill kernel: the VALU decode kernel, one workgroup per
+    // (new token, kv head) over that token's keys (MIP_EUNSUPPORTED past 8 heads per kv head).
+    if (num_cache_blocks > INT32_MAX) return MIP_EINVAL;
+    return decode::valu_prefill_launch(out, out_stride_tok, out_stride_head, q, q_stride_tok, q_stride_head, k_cache,
+                                       v_cache, num_cache_blocks, block_tables, bt_stride, cu_q, ctx_start, num_seqs,
+                                       max_q_len, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq,
+                                       scale, dtype, static_cast<hipStream_t>(stream));
+  }
   // q rows are read and output rows written 16 / 8 bytes at a time.
   const uint64_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
                          static_cast<uint64_t>(q_stride_tok * 2) | static_cast<uint64_t>(q_stride_head * 2) |

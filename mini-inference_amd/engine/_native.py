@@ -14,10 +14,12 @@ LIB_PATH = Path(__file__).resolve().parent / "libmipaged.so"
 
 MIP_F32, MIP_F16, MIP_BF16 = 0, 1, 2
 MIP_OK, MIP_EINVAL, MIP_EUNSUPPORTED = 0, -22, -95
+MIP_ALGO = {"auto": 0, "valu": 1, "mfma": 2, "stream": 3}
 
 EXPORTED = (
     "mip_version",
     "mip_status_string",
+    "mip_set_decode_algo",
     "mip_kv_append",
     "mip_rope_kv_append",
     "mip_paged_decode",
@@ -29,12 +31,16 @@ EXPORTED = (
     "mip_copy_blocks",
 )
 
+# Measurement helpers in the same library (include/mipaged_probe.h), outside the drop-in ABI.
+PROBE_EXPORTED = ("mip_hbm_read_probe",)
+
 _c = ctypes
 _i32, _i64, _sz, _vp, _f32 = _c.c_int32, _c.c_int64, _c.c_size_t, _c.c_void_p, _c.c_float
 
 _SIGNATURES = {
     "mip_version": (_c.c_int, []),
     "mip_status_string": (_c.c_char_p, [_c.c_int]),
+    "mip_set_decode_algo": (_c.c_int, [_i32]),
     "mip_kv_append": (
         _c.c_int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
@@ -67,6 +73,7 @@ _SIGNATURES = {
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp],
     ),
     "mip_copy_blocks": (_c.c_int, [_vp, _vp, _vp, _i32, _i32, _i64, _i64, _vp]),
+    "mip_hbm_read_probe": (_c.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _i32, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -98,6 +105,17 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     if path is None:
         _lib = lib
     return lib
+
+
+def set_decode_algo(name: str) -> str:
+    """Force the decode attention algorithm ("auto", "valu", "mfma", "stream"); returns the previous one.
+
+    Process-wide (``mip_set_decode_algo``); meant for kernel comparisons and tests.
+    """
+    prev = load().mip_set_decode_algo(MIP_ALGO[name])
+    if prev < 0:
+        raise NativeError(f"mip_set_decode_algo({name!r}) failed: status {prev}")
+    return next(k for k, v in MIP_ALGO.items() if v == prev)
 
 
 def check(status: int, what: str) -> None:

@@ -88,7 +88,8 @@ class _GraphDecodeContext:
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
         out = paged_ops.paged_decode_append(q[:, :, 0], k[:, :, 0], v[:, :, 0], k_layer, v_layer, self.slot_mapping,
                                             self.tables, self.context_lens, scale=self.scale,
-                                            max_blocks=self.num_blocks, plan=self.plan)
+                                            max_blocks=self.num_blocks, workspace=self.owner.workspace,
+                                            plan=self.plan)
         return out.unsqueeze(2)
 
     def attend_rope(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
@@ -99,7 +100,7 @@ class _GraphDecodeContext:
         paged_ops.rope_kv_append(q1, k[:, :, 0], v[:, :, 0], cos[:, 0, 0], sin[:, 0, 0], k_layer, v_layer,
                                  self.slot_mapping)
         out = paged_ops.paged_decode(q1, k_layer, v_layer, self.tables, self.context_lens, scale=self.scale,
-                                     max_blocks=self.num_blocks, plan=self.plan)
+                                     max_blocks=self.num_blocks, workspace=self.owner.workspace, plan=self.plan)
         return out.unsqueeze(2)
 
 
@@ -144,6 +145,15 @@ class GraphedDecoder:
         self.tables = torch.full((top, dt.max_blocks), cache.scratch_block, dtype=torch.int32, device=dev)
         self.slot_mapping = torch.zeros(top, dtype=torch.long, device=dev)
         self.context_lens = torch.ones(top, dtype=torch.int32, device=dev)
+        # Decode scratch shared by every captured graph: sized for the largest need over all
+        # (batch, kv length) buckets and allocated once, before any capture, so no graph is
+        # ever left holding the address of a buffer that was replaced. (A call with few
+        # sequences can need more than a full batch: its long segments are merged in runs.)
+        hq = model.cfg.num_heads
+        need = max(paged_ops.decode_workspace_bytes(b, hq, cache.num_kv_heads, cache.head_dim, cache.block_size,
+                                                    kv // cache.block_size, cache.k.dtype)
+                   for b in self.batch_buckets for kv in self.kv_buckets)
+        self.workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
         # (batch, kv_len) -> (graph, its output logits, its context); the context stays alive
         # with the graph because the graph reads its tensors.
         self.graphs: dict[tuple[int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor, _GraphDecodeContext]] = {}

@@ -7,9 +7,11 @@ Drop-in for the paged half of the reference's engine/kv_cache.py:
   prefix caching and graph code see the same block ids. It adds :meth:`copy_blocks`
   and :meth:`fork` for copy-on-write of shared blocks.
 * :class:`PagedDecodeContext` (engine/kv_cache.py:582-624): ``attend`` = KV append +
-  paged decode attention in one fused call. No gathered copy of the history is made.
+  paged decode attention in one fused call. No gathered copy of the history is made, and
+  the block tables stay on the device (:class:`DeviceBlockTables`): a step uploads the
+  batch's slot ids, positions and the table entries written since the last step.
 * :class:`PackedPrefillContext` (engine/kv_cache.py:218-301): the packed scatter is the
-  append kernel; the prefill attention itself stays in torch SDPA.
+  append kernel and the attention over cached prefixes is the paged prefill kernel.
 
 Pool layout (reference engine/kv_cache.py:426-428):
 ``k, v: [num_layers, num_blocks + 1, num_kv_heads, block_size, head_dim]``; block
@@ -25,7 +27,7 @@ import numpy as np
 import torch
 
 from . import paged_ops
-from .model import Qwen2Config, sdpa_attention
+from .model import Qwen2Config
 
 
 class PagedKVCache:
@@ -346,13 +348,19 @@ class DeviceBlockTables:
 class PagedDecodeContext:
     """One batched decode step: B sequences, one new token each (engine/kv_cache.py:582-624).
 
-    Built once per step on the host; every layer's ``attend`` reuses its device tensors:
+    Built once per step; every layer's ``attend`` reuses its device tensors:
 
     * ``positions`` int64 ``[B]`` (RoPE positions, where each new token goes);
     * ``slot_mapping`` int64 ``[B]`` = ``write_blocks * block_size + write_offsets``;
-    * ``block_tables`` int32 ``[B, nb]``, rows padded with block 0 like the reference's
-      ``tables`` (``nb`` = blocks of the longest sequence);
+    * ``block_tables`` int32 ``[B, nb]`` (``nb`` = blocks of the longest sequence), gathered
+      on the device from the cache's :class:`DeviceBlockTables`. Entries past a sequence's
+      own blocks are stale, where the reference pads with block 0; no kernel reads them;
     * ``context_lens`` int32 ``[B]`` = ``positions + 1`` (keys each query attends).
+
+    The reference rebuilds the padded tables on the host and copies them every step
+    (engine/kv_cache.py:597-607). Here the host does O(B) work: the batch's slot ids,
+    positions and slots, plus the table entries logged since the previous step, go to the
+    device in one copy; the mirror is updated there and the batch's rows gathered from it.
 
     With ``fuse_rope`` set (the default) the model hands over q and k before the rotary
     embedding and calls :meth:`attend_rope`; otherwise it rotates them itself and calls
@@ -365,27 +373,37 @@ class PagedDecodeContext:
         self.cache = cache
         self.slots = list(slots)
         bs = cache.block_size
-        pos = np.asarray([cache.lengths[s] for s in self.slots], dtype=np.int64)
-        tables = [cache.block_tables[s] for s in self.slots]
-        if any(p // bs >= len(t) for p, t in zip(pos.tolist(), tables)):
+        pos = [cache.lengths[s] for s in self.slots]
+        if any(p // bs >= len(cache.block_tables[s]) for p, s in zip(pos, self.slots)):
             raise ValueError("a sequence has no block for its next token (call ensure_capacity first)")
-        cache.prepare_writes(self.slots, pos.tolist(), [1] * len(self.slots))
-        tables = [cache.block_tables[s] for s in self.slots]  # copy-on-write may have replaced blocks
-        nb = int(pos.max()) // bs + 1 if len(pos) else 1
-        padded = np.zeros((len(self.slots), nb), dtype=np.int32)
-        for i, t in enumerate(tables):
-            row = t[:nb]
-            padded[i, :len(row)] = row
-        write_blocks = padded[np.arange(len(self.slots)), pos // bs].astype(np.int64)
-        write_offsets = pos % bs
-        dev = cache.k.device
-        i64 = torch.from_numpy(np.concatenate([pos, write_blocks, write_offsets, write_blocks * bs + write_offsets]))
-        i64 = i64.to(dev)
+        cache.prepare_writes(self.slots, pos, [1] * len(self.slots))  # copy-on-write of shared blocks
+        dt = cache.enable_device_tables()
         b = len(self.slots)
-        self.positions, self.write_blocks, self.write_offsets, self.slot_mapping = i64.split(b)
-        i32 = torch.from_numpy(np.concatenate([(pos + 1).astype(np.int32), padded.reshape(-1)])).to(dev)
-        self.context_lens = i32[:b]
-        self.block_tables = i32[b:].view(b, nb)
+        write_blocks = [cache.block_tables[s][p // bs] for s, p in zip(self.slots, pos)]
+        flat, blocks = dt.flat_entries(cache.drain_journal())
+        m = len(flat)
+        # One int64 upload: slot ids | positions | slots | journal (flat index, block) | context
+        # lengths as int32 pairs.
+        n32 = (b + 1) // 2
+        stage = np.empty(3 * b + 2 * m + n32, dtype=np.int64)
+        stage[:b] = self.slots
+        stage[b:2 * b] = pos
+        stage[2 * b:3 * b] = np.asarray(write_blocks, dtype=np.int64) * bs + np.asarray(pos, dtype=np.int64) % bs
+        stage[3 * b:3 * b + m] = flat
+        stage[3 * b + m:3 * b + 2 * m] = blocks
+        lens32 = stage[3 * b + 2 * m:].view(np.int32)
+        lens32[:b] = np.asarray(pos, dtype=np.int32) + 1
+        lens32[b:] = 0
+        dev = cache.k.device
+        staged = torch.from_numpy(stage).to(dev)
+        row_ids = staged[:b]
+        self.positions = staged[b:2 * b]
+        self.slot_mapping = staged[2 * b:3 * b]
+        if m:
+            dt.rows.view(-1).scatter_(0, staged[3 * b:3 * b + m], staged[3 * b + m:3 * b + 2 * m].to(torch.int32))
+        self.context_lens = staged[3 * b + 2 * m:].view(torch.int32)[:b]
+        nb = max(pos) // bs + 1 if b else 1
+        self.block_tables = torch.index_select(dt.rows[:, :nb], 0, row_ids)
         self.num_blocks = nb
         self.kv_len = nb * bs
         self.scale = 1.0 / (cache.head_dim ** 0.5)
@@ -394,8 +412,18 @@ class PagedDecodeContext:
 
     @property
     def tables(self) -> torch.Tensor:
-        """The padded block tables (int32 here; int64 in the reference)."""
+        """The batch's block tables (int32 here; int64 and zero-padded in the reference)."""
         return self.block_tables
+
+    @property
+    def write_blocks(self) -> torch.Tensor:
+        """Block of each new token (engine/kv_cache.py:603), from ``slot_mapping``."""
+        return torch.div(self.slot_mapping, self.cache.block_size, rounding_mode="floor")
+
+    @property
+    def write_offsets(self) -> torch.Tensor:
+        """Offset of each new token in its block (engine/kv_cache.py:604)."""
+        return self.slot_mapping % self.cache.block_size
 
     @property
     def mask(self) -> torch.Tensor:
@@ -450,9 +478,9 @@ class PackedPrefillContext:
     The scatter of the N packed tokens into the pool is the append kernel. Attention over
     the packed tokens (block-diagonal causal, plus any cached prefix of each sequence) is the
     paged prefill kernel (``mip_paged_prefill``), which reads every key in place through the
-    block tables. Shapes it does not cover (fp32, head_dim other than 64/128) use torch SDPA
-    with the reference's mask and read-back, as the reference does. ``fuse_rope`` as for
-    :class:`PagedDecodeContext`.
+    block tables; there is no SDPA path. A shape the library has no kernel for raises.
+    ``mask`` and ``read_at`` (the reference's dense mask and read-back index) are still built
+    on demand for callers that read them. ``fuse_rope`` as for :class:`PagedDecodeContext`.
     """
 
     fuse_rope = True
@@ -544,20 +572,10 @@ class PackedPrefillContext:
         return self._attention(k_layer, v_layer, q, k, v)
 
     def _attention(self, k_layer, v_layer, q, k, v) -> torch.Tensor:
-        c = self.cache
-        if paged_ops.prefill_supported(c.head_dim, q.shape[1], c.num_kv_heads, q.dtype):
-            # q is [1, Hq, N, D]; the kernel takes the [N, Hq, D] view and returns [N, Hq, D].
-            out = paged_ops.paged_prefill(q[0].transpose(0, 1), k_layer, v_layer, self.block_tables, self.cu_q,
-                                          self.ctx_start, self.max_q_len, scale=1.0 / (c.head_dim ** 0.5))
-            return out.transpose(0, 1).unsqueeze(0)
-        if self.has_prefix:
-            rb, ro = self.read_at
-            keys = k_layer[rb, :, ro].transpose(0, 1).unsqueeze(0)
-            values = v_layer[rb, :, ro].transpose(0, 1).unsqueeze(0)
-            return sdpa_attention(q, keys, values, attn_mask=self.mask)
-        if self.mask is None:
-            return sdpa_attention(q, k, v, is_causal=True)
-        return sdpa_attention(q, k, v, attn_mask=self.mask)
+        # q is [1, Hq, N, D]; the kernel takes the [N, Hq, D] view and returns [N, Hq, D].
+        out = paged_ops.paged_prefill(q[0].transpose(0, 1), k_layer, v_layer, self.block_tables, self.cu_q,
+                                      self.ctx_start, self.max_q_len, scale=1.0 / (self.cache.head_dim ** 0.5))
+        return out.transpose(0, 1).unsqueeze(0)
 
     def commit(self) -> None:
         for slot, start, n in zip(self.slots, self.starts, self.lengths):

@@ -71,20 +71,6 @@ class AttentionContext(Protocol):
     def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor: ...
 
 
-def sdpa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, attn_mask: torch.Tensor | None = None,
-                   is_causal: bool = False) -> torch.Tensor:
-    """GQA attention through torch SDPA, each kv head repeated for its query group.
-
-    Query head h reads kv head h // G (engine/model.py:101-123). Used by the prefill
-    context, whose attention is outside the paged decode path.
-    """
-    group = q.shape[1] // k.shape[1]
-    if group > 1:
-        k = torch.repeat_interleave(k, group, dim=1)
-        v = torch.repeat_interleave(v, group, dim=1)
-    return F.scaled_dot_product_attention(q, k, v, attn_mask=attn_mask, is_causal=is_causal)
-
-
 class RMSNorm(nn.Module):
     """x / rms(x) * weight with the statistic taken in fp32, result cast back first."""
 

@@ -157,12 +157,14 @@ class _Workspace:
 
     Calls that use it must be ordered (one stream, or graph replays on that stream): two
     decode calls running concurrently on different streams of one device would race on
-    it; pass ``workspace=`` to each instead. Allocate it before graph capture (one eager
-    call with the largest shape).
+    it; pass ``workspace=`` to each instead. A buffer that has been handed out is never
+    freed: a captured graph may hold its address, so growing the workspace keeps the old
+    buffer alive (``retired``) for the life of the process.
     """
 
     def __init__(self) -> None:
         self._bufs: dict[int, torch.Tensor] = {}
+        self.retired: list[torch.Tensor] = []
 
     def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
         if nbytes == 0:
@@ -170,6 +172,8 @@ class _Workspace:
         key = device.index if device.index is not None else torch.cuda.current_device()
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                self.retired.append(buf)
             size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
             buf = torch.empty(size, dtype=torch.uint8, device=device)
             self._bufs[key] = buf
@@ -181,8 +185,15 @@ _workspace = _Workspace()
 
 def decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
                            max_blocks: int, dtype: torch.dtype) -> int:
+    """Bytes of scratch a decode call of this shape needs (``mip_paged_decode_workspace``)."""
     return int(_native.load().mip_paged_decode_workspace(batch, num_heads, num_kv_heads, head_dim, block_size,
                                                          max_blocks, dtype_code(dtype)))
+
+
+def _plan_key(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, block_size: int, max_blocks: int,
+              dtype: torch.dtype) -> tuple:
+    """The shape a work plan is laid out for (its tensor carries it as ``_mip_plan_key``)."""
+    return (batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks, dtype)
 
 
 def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
@@ -236,6 +247,10 @@ def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
         _require_device(plan)
         if plan.dtype != torch.int32 or not plan.is_contiguous():
             raise ValueError("plan must be a contiguous int32 tensor from decode_plan")
+        made_for = getattr(plan, "_mip_plan_key", None)
+        want = _plan_key(b, hq, hkv, d, bs, mb, q.dtype)
+        if made_for is not None and made_for != want:
+            raise ValueError(f"the plan was made for shape {made_for}, not this call's {want}")
     plan_ptr = plan.data_ptr() if plan is not None else None
     plan_bytes = plan.numel() * 4 if plan is not None else 0
     args = (out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1),
@@ -281,6 +296,7 @@ def prepare_decode_plan(context_lens: torch.Tensor, block_tables: torch.Tensor, 
         plan = torch.empty(-(-need // 4), dtype=torch.int32, device=context_lens.device)
     elif plan.dtype != torch.int32 or not plan.is_contiguous() or plan.numel() * 4 < need:
         raise ValueError(f"plan must be a contiguous int32 tensor of at least {need} bytes")
+    plan._mip_plan_key = _plan_key(b, num_heads, num_kv_heads, head_dim, block_size, mb, dtype)
     args = (context_lens.data_ptr(), block_tables.data_ptr(), block_tables.stride(0), b, num_heads, num_kv_heads,
             head_dim, block_size, mb, code, plan.data_ptr(), plan.numel() * 4, _stream_ptr(context_lens.device))
     keep = (context_lens, block_tables, plan)
@@ -320,26 +336,10 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     return out
 
 
-PREFILL_DTYPES = (torch.float16, torch.bfloat16)
-
-
-def prefill_supported(head_dim: int, num_heads: int, num_kv_heads: int, dtype: torch.dtype) -> bool:
-    """Whether :func:`paged_prefill` has a kernel for this shape (16-bit, D 64/128, group <= 16)."""
-    return (dtype in PREFILL_DTYPES and head_dim in (64, 128) and num_heads % num_kv_heads == 0
-            and num_heads // num_kv_heads <= 16)
-
-
-def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
-                  cu_q: torch.Tensor, ctx_start: torch.Tensor, max_q_len: int, scale: float | None = None,
-                  out: torch.Tensor | None = None, max_blocks: int | None = None) -> torch.Tensor:
-    """Varlen causal attention of packed new tokens over their sequences' paged keys.
-
-    ``q``: ``[N, Hq, D]`` packed rows (last dim contiguous); sequence ``s`` owns rows
-    ``cu_q[s] .. cu_q[s+1]-1`` (int32 ``[S+1]``), at positions ``ctx_start[s] + i``
-    (int32 ``[S]``), and each row attends its sequence's keys ``0 .. position`` read from the
-    pool through ``block_tables`` (int32 ``[S, >= max_blocks]``). Returns ``out [N, Hq, D]``.
-    Follows engine/kv_cache.py:268-294 (prefix read-back + mask) and :290-294 (packed causal).
-    """
+def prepare_paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                          cu_q: torch.Tensor, ctx_start: torch.Tensor, max_q_len: int, scale: float | None = None,
+                          out: torch.Tensor | None = None, max_blocks: int | None = None):
+    """Validate a :func:`paged_prefill` call once; returns ``(PreparedCall, out)``."""
     _require_device(q, k_cache, v_cache, block_tables, cu_q, ctx_start)
     if q.dim() != 3 or q.stride(2) != 1:
         raise ValueError("q must be [N, Hq, D] with a contiguous last dimension")
@@ -361,13 +361,34 @@ def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     nbm = block_tables.shape[1] if max_blocks is None else max_blocks
     if out is None:
         out = torch.empty(n, hq, d, dtype=q.dtype, device=q.device)
-    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    elif out.shape != (n, hq, d) or out.dtype != q.dtype or out.stride(2) != 1:
+        raise ValueError("out must be [N, Hq, D] in q's dtype with a contiguous last dimension")
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
     lib = _native.load()
-    st = lib.mip_paged_prefill(out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1),
-                               k_cache.data_ptr(), v_cache.data_ptr(), nb1, block_tables.data_ptr(),
-                               block_tables.stride(0), cu_q.data_ptr(), ctx_start.data_ptr(), num_seqs, max_q_len, hq,
-                               hkv, d, bs, nbm, scale, dtype_code(q.dtype), _stream_ptr(q.device))
-    _native.check(st, "mip_paged_prefill")
+    args = (out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
+            v_cache.data_ptr(), nb1, block_tables.data_ptr(), block_tables.stride(0), cu_q.data_ptr(),
+            ctx_start.data_ptr(), num_seqs, max_q_len, hq, hkv, d, bs, nbm, scale, dtype_code(q.dtype),
+            _stream_ptr(q.device))
+    keep = (out, q, k_cache, v_cache, block_tables, cu_q, ctx_start)
+    return PreparedCall(lib.mip_paged_prefill, args, "mip_paged_prefill", keep), out
+
+
+def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                  cu_q: torch.Tensor, ctx_start: torch.Tensor, max_q_len: int, scale: float | None = None,
+                  out: torch.Tensor | None = None, max_blocks: int | None = None) -> torch.Tensor:
+    """Varlen causal attention of packed new tokens over their sequences' paged keys.
+
+    ``q``: ``[N, Hq, D]`` packed rows (last dim contiguous); sequence ``s`` owns rows
+    ``cu_q[s] .. cu_q[s+1]-1`` (int32 ``[S+1]``), at positions ``ctx_start[s] + i``
+    (int32 ``[S]``), and each row attends its sequence's keys ``0 .. position`` read from the
+    pool through ``block_tables`` (int32 ``[S, >= max_blocks]``). Returns ``out [N, Hq, D]``.
+    Follows engine/kv_cache.py:268-294 (prefix read-back + mask) and :290-294 (packed causal).
+    16-bit data at head_dim 64/128 runs the MFMA prefill kernel, other shapes (fp32, other
+    head sizes, at most 8 query heads per kv head) the VALU kernel; anything else raises.
+    """
+    call, out = prepare_paged_prefill(q, k_cache, v_cache, block_tables, cu_q, ctx_start, max_q_len, scale, out,
+                                      max_blocks)
+    call()
     return out
 
 
@@ -387,13 +408,8 @@ def paged_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cac
     return out
 
 
-def copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs: torch.Tensor) -> None:
-    """Copy whole blocks, every layer, K and V: ``pool[:, dst] = pool[:, src]`` per (src, dst) row.
-
-    ``k_pool``/``v_pool``: ``[num_layers, num_blocks + 1, Hkv, block_size, D]`` contiguous.
-    ``pairs``: int64 ``[n, 2]`` on the pool's device. Bitwise copy (no reference
-    counterpart; used for copy-on-write of shared prefix blocks).
-    """
+def prepare_copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs: torch.Tensor):
+    """Validate a :func:`copy_blocks` call once; returns a :class:`PreparedCall` (or a no-op for no pairs)."""
     _require_device(k_pool, v_pool, pairs)
     if k_pool.shape != v_pool.shape or k_pool.dim() != 5 or not (k_pool.is_contiguous() and v_pool.is_contiguous()):
         raise ValueError("k_pool/v_pool must be contiguous [L, num_blocks, Hkv, block_size, D] tensors of one shape")
@@ -401,9 +417,19 @@ def copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs: torch.Tensor)
         raise ValueError("pairs must be contiguous int64 [n, 2]")
     n = pairs.shape[0]
     if n == 0:
-        return
+        return _noop
     num_layers, nb = k_pool.shape[0], k_pool.shape[1]
     block_bytes = k_pool[0, 0].numel() * k_pool.element_size()
-    st = _native.load().mip_copy_blocks(k_pool.data_ptr(), v_pool.data_ptr(), pairs.data_ptr(), n, num_layers, nb,
-                                        block_bytes, _stream_ptr(k_pool.device))
-    _native.check(st, "mip_copy_blocks")
+    args = (k_pool.data_ptr(), v_pool.data_ptr(), pairs.data_ptr(), n, num_layers, nb, block_bytes,
+            _stream_ptr(k_pool.device))
+    return PreparedCall(_native.load().mip_copy_blocks, args, "mip_copy_blocks", (k_pool, v_pool, pairs))
+
+
+def copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs: torch.Tensor) -> None:
+    """Copy whole blocks, every layer, K and V: ``pool[:, dst] = pool[:, src]`` per (src, dst) row.
+
+    ``k_pool``/``v_pool``: ``[num_layers, num_blocks + 1, Hkv, block_size, D]`` contiguous.
+    ``pairs``: int64 ``[n, 2]`` on the pool's device. Bitwise copy (no reference
+    counterpart; used for copy-on-write of shared prefix blocks).
+    """
+    prepare_copy_blocks(k_pool, v_pool, pairs)()

@@ -13,7 +13,9 @@ pool-sized fills). The five shapes:
   4  fp16, 64 requests sharing a 520-token prefix (32 full blocks + a partial one, forked,
      so the partial block is copied on write), unique suffixes U[32, 512], packed append
      (:func:`build_prefix_batch`)
-  5  bf16, 28q/4kv heads, D 128, 28 layers, B 128, ctx log-uniform [512, 8192], block 32
+  5  bf16, 28q/4kv heads, D 128, 28 layers, B 128, ctx log-uniform [512, 8192], block 32,
+     tables randomly permuted over a pool of about 60 % of the 288 GB HBM (94,168 blocks of
+     1.835 MB each over the 28 layers' K and V: 172.8 GB)
 
 "ctx" is the number of tokens already cached; a decode step appends one, so a sequence
 attends ctx + 1 keys.
@@ -49,14 +51,24 @@ class DecodeShape:
     table_mode: str = "allocator"  # "chunks" | "permuted" | "allocator"
 
 
+HBM_BYTES = 288e9  # MI355X
+
+
+def pool_blocks_for(fraction: float, num_layers: int, num_kv_heads: int, block_size: int, head_dim: int,
+                    elem_bytes: int) -> int:
+    """Blocks of a pool that fills ``fraction`` of the HBM with every layer's K and V."""
+    per_block = 2 * num_layers * num_kv_heads * block_size * head_dim * elem_bytes
+    return int(fraction * HBM_BYTES // per_block)
+
+
 SHAPES = {
     1: DecodeShape("cfg1-fp32-b8", torch.float32, 1, 14, 2, 64, 16, 8, 16, 256, False, 512, table_mode="chunks"),
     2: DecodeShape("cfg2-fp16-b32", torch.float16, 24, 14, 2, 64, 16, 32, 128, 1024, False, 16384, kv_scale=0.5,
                    table_mode="permuted"),
     3: DecodeShape("cfg3-bf16-b256", torch.bfloat16, 24, 14, 2, 64, 16, 256, 128, 4096, True, 32768,
                    churn_events=5000),
-    5: DecodeShape("cfg5-bf16-b128-d128", torch.bfloat16, 28, 28, 4, 128, 32, 128, 512, 8192, True, 16384,
-                   churn_events=5000),
+    5: DecodeShape("cfg5-bf16-b128-d128", torch.bfloat16, 28, 28, 4, 128, 32, 128, 512, 8192, True,
+                   pool_blocks_for(0.6, 28, 4, 32, 128, 2), table_mode="permuted"),
 }
 
 

@@ -1,0 +1,214 @@
+"""The paged KV-cache path driven through the reference engine's own caller flow, on the GPU.
+
+The reference's scheduler and runner (engine/scheduler.py:64-130, engine/engine.py:93-123 and
+:279-310) use the cache only through its allocator API and two contexts: requests are admitted
+with ``allocate(num_tokens, token_ids)`` (a prefix-cache hit shares blocks), prefilled in one
+packed forward pass over their uncached tokens, registered with ``register_prefix``, then
+decoded one token per step; when ``ensure_capacity`` fails the newest request is preempted
+(``free``) and later recomputes its prompt plus what it had generated. This test restates that
+flow (test infrastructure, not part of the product) over this build's cache and kernels and a
+random-init Qwen2 model, and checks every logit row it produces against each request run alone
+with no prefix caching and no preemption, as tests/test_engine_parity.py:78-116 of the
+reference does with real weights. Tokens are teacher-forced (fixed in advance), so a rounding
+difference can never change which token comes next.
+"""
+
+from __future__ import annotations
+
+import random
+from collections import deque
+from dataclasses import dataclass, field
+
+import pytest
+import torch
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+BS = 16
+# Relative bound on |engine - alone| / max |logit|: the two runs batch the GEMMs differently
+# and, in bf16, round K/V and activations at different batch shapes.
+REL_TOL = {torch.float32: 1e-4, torch.bfloat16: 4e-2}
+
+
+@dataclass
+class Req:
+    rid: int
+    prompt: list[int]
+    forced: list[int]          # the output tokens, fixed in advance
+    arrive: int                # engine step at which the request arrives
+    slot: int | None = None
+    out: list[int] = field(default_factory=list)
+    preemptions: int = 0
+
+    @property
+    def tokens(self) -> list[int]:
+        return self.prompt + self.out
+
+    @property
+    def done(self) -> bool:
+        return len(self.out) >= len(self.forced)
+
+
+def _model(gpu, dtype):
+    from engine.model import Qwen2Config, Qwen2ForCausalLM, random_init_
+
+    cfg = Qwen2Config(vocab_size=512, hidden_size=896, intermediate_size=1024, num_layers=2, num_heads=14,
+                      num_kv_heads=2, head_dim=64)
+    with torch.device(gpu):
+        model = Qwen2ForCausalLM(cfg)
+    return cfg, random_init_(model.to(gpu, dtype), seed=1)
+
+
+def _requests(n=7, seed=0):
+    """Requests 0-4 share a 40-token system prefix (two full blocks of 16), 5-6 do not."""
+    rnd = random.Random(seed)
+    system = [rnd.randrange(512) for _ in range(40)]
+    reqs = []
+    for i in range(n):
+        body = [rnd.randrange(512) for _ in range(rnd.randint(4, 12))]
+        prompt = (system + body) if i < 5 else [rnd.randrange(512) for _ in range(rnd.randint(20, 44))]
+        forced = [rnd.randrange(512) for _ in range(rnd.randint(8, 20))]
+        reqs.append(Req(i, prompt, forced, arrive=i // 2))
+    return reqs
+
+
+def _prefill(model, cache, seqs, gpu):
+    """engine/engine.py:102-109 (prefill_packed) over each sequence's uncached tokens."""
+    new = [s.tokens[cache.lengths[s.slot]:] for s in seqs]
+    ctx = cache.packed_prefill_context([s.slot for s in seqs], [len(t) for t in new])
+    ids = torch.tensor([[t for toks in new for t in toks]], device=gpu)
+    hidden = model(ids, ctx.positions.unsqueeze(0), ctx)
+    ctx.commit()
+    return model.compute_logits(hidden[0, ctx.last_index]).float()
+
+
+def _decode(model, cache, seqs, gpu):
+    """engine/engine.py:111-123 (decode) without graphs."""
+    ctx = cache.decode_context([s.slot for s in seqs])
+    ids = torch.tensor([s.tokens[-1] for s in seqs], device=gpu).unsqueeze(1)
+    hidden = model(ids, ctx.positions.unsqueeze(1), ctx)
+    ctx.commit()
+    return model.compute_logits(hidden[:, -1]).float()
+
+
+@torch.inference_mode()
+def _alone(model, cfg, req, gpu, dtype):
+    """The request by itself: no prefix caching, a pool that never runs out. Returns
+    {position of the last processed token: logits}."""
+    from engine.kv_cache import PagedKVCache
+
+    cache = PagedKVCache.for_model(cfg, num_blocks=16, block_size=BS, max_seqs=1, max_len=128, dtype=dtype,
+                                   device=gpu)
+    r = Req(req.rid, req.prompt, req.forced, 0)
+    r.slot = cache.allocate(len(r.prompt))
+    logits = {}
+    row = _prefill(model, cache, [r], gpu)[0]
+    while True:
+        logits[len(r.tokens) - 1] = row
+        r.out.append(r.forced[len(r.out)])
+        if r.done:
+            break
+        assert cache.ensure_capacity(r.slot, len(r.tokens))
+        row = _decode(model, cache, [r], gpu)[0]
+    cache.free(r.slot)
+    return logits
+
+
+@torch.inference_mode()
+def _engine(model, cfg, reqs, gpu, dtype, num_blocks, max_seqs=3, max_batched=512):
+    """Continuous batching with prefix caching and preemption by recompute
+    (engine/scheduler.py:64-130 restated; engine/engine.py:279-310 for one step)."""
+    from engine.kv_cache import PagedKVCache
+
+    cache = PagedKVCache.for_model(cfg, num_blocks=num_blocks, block_size=BS, max_seqs=max_seqs, max_len=128,
+                                   dtype=dtype, device=gpu, enable_prefix_caching=True)
+    pending = deque(sorted(reqs, key=lambda r: r.arrive))
+    waiting: deque[Req] = deque()
+    running: list[Req] = []
+    logits: dict[tuple[int, int], torch.Tensor] = {}
+    preemptions = 0
+    step = 0
+
+    def preempt(victim: Req) -> None:
+        nonlocal preemptions
+        running.remove(victim)
+        cache.free(victim.slot)
+        victim.slot = None
+        victim.preemptions += 1
+        waiting.appendleft(victim)
+        preemptions += 1
+
+    def emit(seqs, rows) -> None:
+        for s, row in zip(seqs, rows):
+            logits[(s.rid, len(s.tokens) - 1)] = row
+            s.out.append(s.forced[len(s.out)])
+            if s.done:
+                running.remove(s)
+                cache.free(s.slot)
+                s.slot = None
+
+    while pending or waiting or running:
+        while pending and pending[0].arrive <= step:
+            waiting.append(pending.popleft())
+        # Scheduler._make_room_for_decodes: room for every running sequence's next token.
+        for s in list(running):
+            if s not in running:
+                continue
+            while not cache.ensure_capacity(s.slot, len(s.tokens)):
+                victim = running[-1]
+                preempt(victim)
+                if victim is s:
+                    break
+        decodes = list(running)
+        budget = max_batched - len(decodes)
+        prefills = []
+        while waiting and len(running) < max_seqs:
+            s = waiting[0]
+            n = len(s.tokens)
+            if n > budget or not cache.can_allocate(n + 1):
+                break
+            waiting.popleft()
+            s.slot = cache.allocate(n, token_ids=s.tokens)
+            running.append(s)
+            prefills.append(s)
+            budget -= n - cache.lengths[s.slot]
+        if prefills:
+            rows = _prefill(model, cache, prefills, gpu)
+            for s in prefills:
+                cache.register_prefix(s.slot, s.tokens)
+            emit(prefills, rows)
+        if decodes:
+            emit(decodes, _decode(model, cache, decodes, gpu))
+        step += 1
+        assert step < 500, "the flow did not finish"
+    return cache, logits, preemptions
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("tiny_pool", [False, True], ids=["roomy-pool", "tiny-pool"])
+def test_engine_flow_matches_requests_alone(gpu, dtype, tiny_pool):
+    """Prefix hits through allocate(token_ids) / register_prefix, packed prefill over shared
+    blocks, decode steps, free; with a 7-block pool, also preemption by recompute. Every logit
+    row matches the request run alone."""
+    announce(f"engine flow {dtype} tiny_pool={tiny_pool}")
+    cfg, model = _model(gpu, dtype)
+    reqs = _requests()
+    want = {r.rid: _alone(model, cfg, r, gpu, dtype) for r in reqs}
+    num_blocks = 7 if tiny_pool else 64
+    cache, got, preemptions = _engine(model, cfg, reqs, gpu, dtype, num_blocks)
+    assert cache.prefix_hit_tokens > 0, "the shared system prompt was meant to hit the prefix cache"
+    if tiny_pool:
+        assert preemptions > 0, "the 7-block pool was meant to force preemption"
+    assert cache.num_free_blocks == num_blocks and not cache.block_tables
+    expected_keys = {(r.rid, p) for r in reqs for p in want[r.rid]}
+    assert set(got) >= expected_keys
+    worst = 0.0
+    for (rid, pos), row in got.items():
+        ref_row = want[rid][pos]
+        err = (row - ref_row).abs().max().item() / ref_row.abs().max().item()
+        worst = max(worst, err)
+        assert err <= REL_TOL[dtype], f"request {rid} position {pos}: relative error {err:.3g}"
+    print(f"engine flow {dtype} tiny_pool={tiny_pool}: {len(got)} logit rows, worst relative error {worst:.3g}, "
+          f"{preemptions} preemptions, {cache.prefix_hit_tokens} prefix-hit tokens")

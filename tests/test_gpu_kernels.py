@@ -211,11 +211,13 @@ def _check_decode(gpu, dtype, batch, hq, hkv, d, bs, lens, seed=0, stale=None, m
 
 
 @pytest.fixture(params=["default", "valu", "mfma", "stream"])
-def algo(request, monkeypatch):
-    """Which partition kernel the library picks (MIP_DECODE_ALGO; ignored where a kernel does not apply)."""
-    if request.param != "default":
-        monkeypatch.setenv("MIP_DECODE_ALGO", request.param)
-    return request.param
+def algo(request):
+    """Which decode kernel the library runs (mip_set_decode_algo; ignored where a kernel does not apply)."""
+    from engine import _native
+
+    prev = _native.set_decode_algo("auto" if request.param == "default" else request.param)
+    yield request.param
+    _native.set_decode_algo(prev)
 
 
 @pytest.mark.parametrize("dtype", list(DTYPES))
@@ -480,8 +482,9 @@ def test_paged_decode_golden_fixture(gpu):
 
 @pytest.mark.parametrize("cfg", [2, 3, 5])
 def test_decode_step_full_size(gpu, cfg):
-    """Configs 2 (fp16 B=32), 3 (bf16 B=256, churned pool) and 5 (bf16 28q/4kv D=128 BS=32 B=128):
-    one layer's append + attention vs float64."""
+    """Configs 2 (fp16 B=32), 3 (bf16 B=256, churned pool) and 5 (bf16 28q/4kv D=128 BS=32 B=128,
+    tables permuted over one layer of the 94k-block pool): one layer's append + attention vs
+    float64."""
     from engine import workloads
 
     announce(f"config{cfg} decode step")
@@ -493,8 +496,12 @@ def test_decode_step_full_size(gpu, cfg):
     ctx = cache.decode_context(batch.slots)
     out = ctx.attend(0, q, k, v)
     torch.cuda.synchronize()
-    tables = [list(cache.block_tables[s]) for s in batch.slots]
-    kp, vp = values(cache.k[0]), values(cache.v[0])
+    # The oracle reads a compact copy of the blocks the batch owns (config 5's pool is 94k blocks).
+    used = sorted({b for s in batch.slots for b in cache.block_tables[s]})
+    remap = {b: i for i, b in enumerate(used)}
+    tables = [[remap[b] for b in cache.block_tables[s]] for s in batch.slots]
+    idx = torch.tensor(used, device=gpu)
+    kp, vp = values(cache.k[0].index_select(0, idx)), values(cache.v[0].index_select(0, idx))
     lens = [n + 1 for n in batch.ctx]
     # the append wrote the new rows where the reference index math says
     inputs = ref.decode_inputs(batch.ctx, tables, cache.block_size)
@@ -582,6 +589,7 @@ def test_decode_context_matches_per_sequence_sdpa(gpu):
     assert [cache.lengths[s] for s in slots] == [7, 10, 4]
 
 
+@torch.inference_mode()
 def test_paged_decode_graph_replay(gpu):
     """Append + attention captured in a HIP graph: every replay equals the eager result."""
     from engine import paged_ops
@@ -597,14 +605,15 @@ def test_paged_decode_graph_replay(gpu):
     k_new = torch.randn(4, 2, 64, device=gpu).to(torch.bfloat16)
     v_new = torch.randn(4, 2, 64, device=gpu).to(torch.bfloat16)
     out = torch.empty_like(qg)
-    eager = paged_ops.paged_decode(qg, kg, vg, btg, cl)  # also allocates the workspace outside capture
+    ws = torch.empty(paged_ops.decode_workspace_bytes(4, 14, 2, 64, 16, width, torch.bfloat16), dtype=torch.uint8,
+                     device=gpu)
     paged_ops.kv_append(kg, vg, k_new, v_new, slots)
-    eager = paged_ops.paged_decode(qg, kg, vg, btg, cl).clone()
+    eager = paged_ops.paged_decode(qg, kg, vg, btg, cl, workspace=ws).clone()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         paged_ops.kv_append(kg, vg, k_new, v_new, slots)
-        paged_ops.paged_decode(qg, kg, vg, btg, cl, out=out)
+        paged_ops.paged_decode(qg, kg, vg, btg, cl, out=out, workspace=ws)
     for i in range(4):
         out.zero_()
         torch.cuda.synchronize()
@@ -612,3 +621,153 @@ def test_paged_decode_graph_replay(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i} differs"
         _ = (qg.float() * 2).sum().item()  # unrelated eager work between replays
+
+
+@torch.inference_mode()
+def test_planned_fused_decode_graph_replay_config3_padded_matches_oracle(gpu):
+    """The graphed decode's attention call at the config-3 shape (bf16, 14q/2kv heads d64,
+    block 16, churned pool): 250 sequences padded to a bucket of 256 with rows on the scratch
+    block, the step's plan and the fused append + attention captured in one graph. Every
+    replay's outputs match the float64 oracle, and the pool (scratch block aside) equals the
+    oracle's append of the new rows, bit for bit."""
+    from engine import paged_ops, workloads
+
+    announce("graph replay config-3 shape, 250 sequences in a 256 bucket, vs oracle")
+    shape = workloads.DecodeShape(**{**workloads.SHAPES[3].__dict__, "num_layers": 1})
+    batch = workloads.build_decode_batch(shape, gpu, seed=0)
+    cache, bs = batch.cache, shape.block_size
+    real, top = 250, 256
+    slots = batch.slots[:real]
+    ctx_lens = batch.ctx[:real]
+    tables = [list(cache.block_tables[s]) for s in slots]
+    nb = max(len(t) for t in tables)
+    bt = np.full((top, nb), cache.scratch_block, dtype=np.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = t
+    lens = np.ones(top, dtype=np.int32)
+    lens[:real] = np.asarray(ctx_lens) + 1
+    slot_map = np.full(top, cache.scratch_block * bs, dtype=np.int64)
+    for i, (t, n) in enumerate(zip(tables, ctx_lens)):
+        slot_map[i] = t[n // bs] * bs + n % bs
+    gen = torch.Generator().manual_seed(31)
+    q = torch.randn(top, 14, 64, generator=gen).to(torch.bfloat16).to(gpu)
+    k_new = torch.randn(top, 2, 64, generator=gen).to(torch.bfloat16).to(gpu)
+    v_new = torch.randn(top, 2, 64, generator=gen).to(torch.bfloat16).to(gpu)
+    bt_t, lens_t = torch.from_numpy(bt).to(gpu), torch.from_numpy(lens).to(gpu)
+    slot_t = torch.from_numpy(slot_map).to(gpu)
+    k_layer, v_layer = cache.k[0], cache.v[0]
+    k_before, v_before = storage(k_layer), storage(v_layer)
+    ws = torch.empty(paged_ops.decode_workspace_bytes(top, 14, 2, 64, bs, nb, torch.bfloat16), dtype=torch.uint8,
+                     device=gpu)
+    out = torch.empty(top, 14, 64, dtype=torch.bfloat16, device=gpu)
+    plan_call, plan = paged_ops.prepare_decode_plan(lens_t, bt_t, 14, 2, 64, bs, torch.bfloat16, max_blocks=nb)
+    assert plan is not None
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_ops.decode_plan(lens_t, bt_t, 14, 2, 64, bs, torch.bfloat16, max_blocks=nb, plan=plan)
+        paged_ops.paged_decode_append(q, k_new, v_new, k_layer, v_layer, slot_t, bt_t, lens_t, max_blocks=nb,
+                                      workspace=ws, plan=plan, out=out)
+    torch.cuda.synchronize()
+    want_k, want_v = k_before.copy(), v_before.copy()
+    ref.append(want_k, want_v, slot_map[:real] // bs, slot_map[:real] % bs, storage(k_new[:real]),
+               storage(v_new[:real]))
+    want = None
+    sc = cache.scratch_block
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        kp, vp = storage(k_layer), storage(v_layer)
+        assert np.array_equal(kp[:sc], want_k[:sc]) and np.array_equal(vp[:sc], want_v[:sc]), f"replay {i}: pool"
+        if want is None:
+            want = ref.attention_f64(values(q[:real]), values(k_layer), values(v_layer), tables,
+                                     lens[:real].tolist(), bs)
+        got = values(out[:real])
+        err = attention_error(got, want, "bfloat16")
+        assert np.isfinite(got).all() and err <= TOL["bfloat16"], f"replay {i}: {err}"
+        _ = (q.float() * 2).sum().item()  # unrelated eager work between replays
+
+
+def test_mismatched_plan_fails_visibly(gpu):
+    """A plan made for another batch: the Python layer refuses it, and through the C ABI the
+    call writes NaN to every output row and leaves the pool unchanged (no silent garbage)."""
+    from engine import paged_ops
+
+    announce("decode with a plan of another batch size")
+    lens = [40, 700, 1300, 5]
+    q, k_pool, v_pool, tables, bt, width = _random_case("bfloat16", 4, 14, 2, 64, 16, lens, seed=23)
+    qg, kg, vg = q.to(gpu), k_pool.to(gpu), v_pool.to(gpu)
+    btg = torch.from_numpy(bt).to(gpu)
+    cl = torch.tensor(lens, dtype=torch.int32, device=gpu)
+    slots = torch.tensor([tables[i][(n - 1) // 16] * 16 + (n - 1) % 16 for i, n in enumerate(lens)],
+                         dtype=torch.int64, device=gpu)
+    k_new = torch.randn(4, 2, 64, device=gpu).to(torch.bfloat16)
+    v_new = torch.randn(4, 2, 64, device=gpu).to(torch.bfloat16)
+    lib = paged_ops._native.load()
+    need4 = lib.mip_paged_decode_plan_bytes(4, 14, 2, 64, 16, width, paged_ops.dtype_code(torch.bfloat16))
+    need3 = lib.mip_paged_decode_plan_bytes(3, 14, 2, 64, 16, width, paged_ops.dtype_code(torch.bfloat16))
+    buf = torch.zeros(-(-max(need4, need3) // 4), dtype=torch.int32, device=gpu)
+    paged_ops.decode_plan(cl[:3], btg[:3], 14, 2, 64, 16, torch.bfloat16, max_blocks=width, plan=buf)
+    with pytest.raises(ValueError, match="plan was made for"):
+        paged_ops.paged_decode_append(qg, k_new, v_new, kg, vg, slots, btg, cl, max_blocks=width, plan=buf)
+    del buf._mip_plan_key  # reach the library as a caller of the C ABI would
+    before_k, before_v = kg.clone(), vg.clone()
+    out = paged_ops.paged_decode_append(qg, k_new, v_new, kg, vg, slots, btg, cl, max_blocks=width, plan=buf)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all(), "a mismatched plan must not leave plausible outputs"
+    assert torch.equal(kg, before_k) and torch.equal(vg, before_v), "a mismatched plan must not append"
+
+
+@torch.inference_mode()
+def test_eager_decode_context_device_tables_match_oracle(gpu):
+    """The eager PagedDecodeContext on the device-resident tables: 40 steps over 8 sequences
+    that cross block boundaries, a sequence freed and its slot reused at step 12, a fork with
+    copy-on-write of its shared partial block at step 24. Each step's outputs match the float64
+    oracle over the host tables, and the pool equals the oracle's append, bit for bit."""
+    from engine.kv_cache import PagedKVCache
+
+    announce("eager decode context, device tables under growth, slot reuse and fork, vs oracle")
+    lengths = [13, 30, 47, 5, 62, 16, 31, 100]
+    cache = PagedKVCache(1, 2, 64, num_blocks=160, block_size=16, max_seqs=16, max_len=512, dtype=torch.bfloat16,
+                         device=gpu)
+    slots = []
+    for n in lengths:
+        s = cache.allocate(n + 1)
+        cache.lengths[s] = n
+        slots.append(s)
+    gen = torch.Generator(device=gpu).manual_seed(2)
+    cache.k.normal_(0.0, 1.0, generator=gen)
+    cache.v.normal_(0.0, 1.0, generator=gen)
+    for step in range(40):
+        if step == 12:
+            cache.free(slots[3])
+            s = cache.allocate(40)
+            cache.lengths[s] = 33
+            slots[3] = s
+        if step == 24:
+            cache.free(slots[5])
+            slots[5] = cache.fork(slots[2])
+        for s in slots:
+            assert cache.ensure_capacity(s, cache.lengths[s] + 1)
+        pos = [cache.lengths[s] for s in slots]
+        ctx = cache.decode_context(slots)  # copy-on-write happens here
+        tables = [list(cache.block_tables[s]) for s in slots]
+        k_before, v_before = storage(cache.k[0]), storage(cache.v[0])
+        q = torch.randn(8, 14, 1, 64, generator=gen, device=gpu).to(torch.bfloat16)
+        k = torch.randn(8, 2, 1, 64, generator=gen, device=gpu).to(torch.bfloat16)
+        v = torch.randn(8, 2, 1, 64, generator=gen, device=gpu).to(torch.bfloat16)
+        out = ctx.attend(0, q, k, v)
+        torch.cuda.synchronize()
+        blocks = np.asarray([t[p // 16] for t, p in zip(tables, pos)])
+        offs = np.asarray(pos) % 16
+        ref.append(k_before, v_before, blocks, offs, storage(k[:, :, 0]), storage(v[:, :, 0]))
+        assert np.array_equal(storage(cache.k[0]), k_before), f"step {step}: K pool"
+        assert np.array_equal(storage(cache.v[0]), v_before), f"step {step}: V pool"
+        want = ref.attention_f64(values(q[:, :, 0]), values(cache.k[0]), values(cache.v[0]), tables,
+                                 [p + 1 for p in pos], 16)
+        err = attention_error(values(out[:, :, 0]), want, "bfloat16")
+        assert err <= TOL["bfloat16"], f"step {step}: {err}"
+        ctx.commit()
+    assert cache.cow_copies >= 1

@@ -1,9 +1,10 @@
 """GPU parity of the paged prefill attention kernel (``mip_paged_prefill``) through the C ABI.
 
 Bar: within 2e-3 beyond the output's own final rounding (half an ulp) of the float64 oracle
-(oracle/paged_ref.py ``prefill_attention_f64``) on the same 16-bit inputs, as for decode.
-The cache context's kernel path also matches the reference's own path (prefix read-back +
-dense mask + SDPA, engine/kv_cache.py:262-294).
+(oracle/paged_ref.py ``prefill_attention_f64``) on the same 16-bit inputs, as for decode;
+2e-5 for fp32 (the VALU path). The cache context's output also matches the reference's own
+formulation (prefix read-back + dense mask + SDPA, engine/kv_cache.py:262-294) evaluated by
+the oracle on the CPU.
 """
 
 from __future__ import annotations
@@ -19,8 +20,9 @@ from oracle import paged_ref as ref
 
 pytestmark = pytest.mark.gpu
 
-DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16}
-MANTISSA_BITS = {"float16": 10, "bfloat16": 7}
+DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
+MANTISSA_BITS = {"float16": 10, "bfloat16": 7, "float32": 23}
+TOL = {"float16": 2e-3, "bfloat16": 2e-3, "float32": 2e-5}
 
 
 def half_ulp(x: np.ndarray, dtype: str) -> np.ndarray:
@@ -73,7 +75,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("d,hq,hkv,bs", [(64, 14, 2, 16), (128, 28, 4, 32), (64, 8, 8, 16), (64, 16, 1, 16),
                                          (128, 7, 1, 4)])
 @pytest.mark.parametrize("case", range(len(CASES)))
@@ -90,7 +92,51 @@ def test_paged_prefill_matches_f64(gpu, dtype, d, hq, hkv, bs, case):
     assert err <= 2e-3, err
 
 
-@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("dtype,d,hq,hkv,bs", [("float32", 64, 14, 2, 16), ("float32", 128, 8, 2, 32),
+                                               ("float16", 32, 8, 2, 16), ("bfloat16", 256, 4, 2, 16),
+                                               ("float32", 8, 4, 4, 4), ("float16", 16, 5, 1, 2)])
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_paged_prefill_valu_shapes(gpu, dtype, d, hq, hkv, bs, case):
+    """Shapes without an MFMA prefill kernel (fp32, head sizes other than 64/128) run the VALU
+    decode kernel, one workgroup per (new token, kv head); same bar against float64."""
+    from engine import paged_ops
+
+    starts, lengths = CASES[case]
+    announce(f"paged_prefill VALU {dtype} d={d} hq={hq} hkv={hkv} bs={bs} starts={starts} lengths={lengths}")
+    dev, want = build(gpu, dtype, d, hq, hkv, bs, starts, lengths, seed=case + 40)
+    out = paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], max(lengths))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    err = float((np.abs(got - want) - half_ulp(want, dtype)).max())
+    assert err <= TOL[dtype], err
+
+
+def test_paged_prefill_valu_stale_rows_and_loose_grid(gpu):
+    """VALU path: NaN rows past every sequence's keys never leak; a loose max_q_len and an empty
+    sequence write nothing extra."""
+    from engine import paged_ops
+
+    announce("paged_prefill VALU fp32 stale NaN rows, loose max_q_len, empty sequence")
+    starts, lengths = [21, 0, 7, 3], [11, 29, 0, 2]
+    dev, want = build(gpu, "float32", 64, 14, 2, 16, starts, lengths, seed=8, stale_nan=True)
+    out = paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], 100)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert float((np.abs(got - want) - half_ulp(want, "float32")).max()) <= TOL["float32"]
+
+
+def test_paged_prefill_unsupported_shape_raises(gpu):
+    """No kernel for fp32 with more than 8 query heads per kv head: the call raises (no fallback)."""
+    from engine import _native, paged_ops
+
+    announce("paged_prefill fp32 group 16: unsupported")
+    dev, _ = build(gpu, "float32", 64, 16, 1, 16, [0], [4], seed=1)
+    with pytest.raises(_native.NativeError, match="unsupported"):
+        paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], 4)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_paged_prefill_never_reads_stale_rows(gpu, dtype):
     from engine import paged_ops
 
@@ -161,42 +207,45 @@ def test_paged_prefill_config4_prefix_hits(gpu):
         assert err <= 2e-3, (s, err)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
 @pytest.mark.parametrize("prefix", [False, True])
 @torch.inference_mode()
-def test_prefill_context_kernel_matches_reference_path(gpu, prefix, monkeypatch):
-    """PackedPrefillContext: the kernel path against the reference's read-back + mask SDPA path."""
-    from engine import paged_ops
+def test_prefill_context_matches_reference_formulation(gpu, prefix, dtype):
+    """PackedPrefillContext.attend (append + paged prefill kernel) against the reference's own
+    formulation, prefix read-back + dense mask + SDPA (engine/kv_cache.py:262-294), which the
+    oracle evaluates in fp32 on the CPU over the pool the context appended to."""
     from engine.kv_cache import PagedKVCache
 
-    announce(f"prefill context kernel vs reference SDPA path, prefix={prefix}")
-    dt, d, hq, hkv, bs = torch.bfloat16, 64, 14, 2, 16
+    announce(f"prefill context vs the reference formulation, prefix={prefix} {dtype}")
+    dt, d, hq, hkv, bs = DTYPES[dtype], 64, 14, 2, 16
     starts = [40, 0, 17] if prefix else [0, 0, 0]
     new = [23, 50, 9]
-    outs = []
-    for use_kernel in (True, False):
-        cache = PagedKVCache(1, hkv, d, num_blocks=64, block_size=bs, max_seqs=4, max_len=256, dtype=dt, device=gpu)
-        slots = []
-        for st, n in zip(starts, new):
-            s = cache.allocate(st + n)
-            cache.lengths[s] = st
-            slots.append(s)
-        gen = torch.Generator(device=gpu).manual_seed(5)
-        cache.k.normal_(0.0, 1.0, generator=gen)
-        cache.v.normal_(0.0, 1.0, generator=gen)
-        ctx = cache.packed_prefill_context(slots, new)
-        n = sum(new)
-        qkv = torch.randn(1, n, (hq + 2 * hkv) * d, generator=gen, device=gpu).to(dt)
-        q, k, v = qkv.split([hq * d, hkv * d, hkv * d], dim=-1)
-        q = q.view(1, n, hq, d).transpose(1, 2)
-        k = k.view(1, n, hkv, d).transpose(1, 2)
-        v = v.view(1, n, hkv, d).transpose(1, 2)
-        if not use_kernel:
-            monkeypatch.setattr(paged_ops, "prefill_supported", lambda *a: False)
-        outs.append(ctx.attend(0, q, k, v).float())
-        monkeypatch.undo()
+    cache = PagedKVCache(1, hkv, d, num_blocks=64, block_size=bs, max_seqs=4, max_len=256, dtype=dt, device=gpu)
+    slots = []
+    for st, n in zip(starts, new):
+        s = cache.allocate(st + n)
+        cache.lengths[s] = st
+        slots.append(s)
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    cache.k.normal_(0.0, 1.0, generator=gen)
+    cache.v.normal_(0.0, 1.0, generator=gen)
+    ctx = cache.packed_prefill_context(slots, new)
+    n = sum(new)
+    qkv = torch.randn(1, n, (hq + 2 * hkv) * d, generator=gen, device=gpu).to(dt)
+    q, k, v = qkv.split([hq * d, hkv * d, hkv * d], dim=-1)
+    q = q.view(1, n, hq, d).transpose(1, 2)
+    k = k.view(1, n, hkv, d).transpose(1, 2)
+    v = v.view(1, n, hkv, d).transpose(1, 2)
+    got = ctx.attend(0, q, k, v).float().cpu()
     torch.cuda.synchronize()
-    err = (outs[0] - outs[1]).abs().max().item()
-    assert err <= 1.6e-2, err  # both sides round to bf16; the reference path also rounds P and its sums
+    tables = [list(cache.block_tables[s]) for s in slots]
+    want = ref.packed_prefill_torch(q.float().cpu(), cache.k[0].float().cpu(), cache.v[0].float().cpu(), tables,
+                                    starts, new, bs)
+    w = want.numpy()
+    err = float((np.abs(got.numpy() - w) - half_ulp(w, dtype)).max())
+    assert err <= TOL[dtype], err
+    ctx.commit()
+    assert [cache.lengths[s] for s in slots] == [a + b for a, b in zip(starts, new)]
 
 
 def test_paged_prefill_grid_fallbacks(gpu):

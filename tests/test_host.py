@@ -23,6 +23,7 @@ from oracle import paged_ref as ref
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "mipaged.h"
+PROBE_HEADER = ROOT / "include" / "mipaged_probe.h"
 
 
 def tiny_paged(num_blocks=12, block_size=4, max_seqs=4, max_len=32, **kw) -> PagedKVCache:
@@ -111,7 +112,12 @@ def test_decode_context_matches_oracle_inputs():
     assert ctx.write_blocks.tolist() == want["write_blocks"].tolist()
     assert ctx.write_offsets.tolist() == want["write_offsets"].tolist()
     assert ctx.context_lens.tolist() == want["context_lens"].tolist()
-    assert ctx.block_tables.tolist() == want["tables"].tolist()
+    # The device-resident rows hold each sequence's blocks; entries past them are stale (the
+    # reference pads with block 0) and no kernel reads them.
+    assert ctx.block_tables.shape == want["tables"].shape
+    for row, t, n in zip(ctx.block_tables.tolist(), want["tables"].tolist(), lengths):
+        used = n // 4 + 1
+        assert row[:used] == t[:used]
     assert ctx.block_tables.dtype == torch.int32 and ctx.context_lens.dtype == torch.int32
     assert torch.equal(ctx.mask, torch.as_tensor(want["mask"])[:, None, None, :])
     ctx.commit()
@@ -219,8 +225,8 @@ def test_packed_prefill_slot_mapping():
 # ----------------------------------------------------------------------------- C ABI
 
 
-def header_functions() -> list[str]:
-    text = HEADER.read_text()
+def header_functions(header=None) -> list[str]:
+    text = (HEADER if header is None else header).read_text()
     return re.findall(r"^\s*(?:const\s+char\s*\*|int|size_t)\s+(mip_\w+)\s*\(", text, flags=re.M)
 
 
@@ -236,12 +242,13 @@ def lib():
 
 def test_header_declares_the_bound_entry_points():
     assert sorted(header_functions()) == sorted(_native.EXPORTED)
+    assert sorted(header_functions(PROBE_HEADER)) == sorted(_native.PROBE_EXPORTED)
 
 
 def test_library_exports_every_declared_symbol(lib):
     raw = ctypes.CDLL(str(_native.LIB_PATH))
-    for name in header_functions():
-        assert hasattr(raw, name), f"{name} declared in mipaged.h but not exported"
+    for name in header_functions() + header_functions(PROBE_HEADER):
+        assert hasattr(raw, name), f"{name} declared in a header but not exported"
     assert lib.mip_version() >> 16 == 0 and lib.mip_version() & 0xFFFF >= 1
     assert lib.mip_status_string(_native.MIP_OK) == b"ok"
     assert lib.mip_status_string(_native.MIP_EINVAL) == b"invalid argument"
@@ -307,6 +314,19 @@ def test_abi_host_checks_return_before_launch(lib):
     assert cp(None, None, None, 0, 24, 100, 8192, None) == OK
     assert cp(None, None, None, 3, 0, 100, 8192, None) == E
     assert cp(None, None, None, 3, 24, 100, 8192, None) == E
+
+
+def test_decode_algo_setting(lib):
+    """mip_set_decode_algo: returns the previous setting, refuses unknown values, host-only."""
+    prev = _native.set_decode_algo("valu")
+    try:
+        assert _native.set_decode_algo("mfma") == "valu"
+        assert _native.set_decode_algo("stream") == "mfma"
+        assert lib.mip_set_decode_algo(7) == _native.MIP_EINVAL
+        assert lib.mip_set_decode_algo(-1) == _native.MIP_EINVAL
+        assert _native.set_decode_algo("auto") == "stream"
+    finally:
+        _native.set_decode_algo(prev)
 
 
 # ----------------------------------------------------------------------------- no CPU fallback
