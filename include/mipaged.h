@@ -45,7 +45,7 @@ extern "C" {
 
 enum mip_dtype { MIP_F32 = 0, MIP_F16 = 1, MIP_BF16 = 2 };
 
-enum mip_status { MIP_OK = 0, MIP_EINVAL = -22, MIP_EUNSUPPORTED = -95 };
+enum mip_status { MIP_OK = 0, MIP_E2BIG = -7, MIP_EINVAL = -22, MIP_EUNSUPPORTED = -95 };
 
 /* Library version, (major << 16) | minor. */
 int mip_version(void);
@@ -201,6 +201,35 @@ int mip_paged_decode_append(const void* k_new, const void* v_new,
                             int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
                             float scale, void* workspace, size_t workspace_bytes,
                             const void* plan, size_t plan_bytes, int32_t dtype, void* stream);
+
+/*
+ * mip_paged_decode_append without a workspace argument: the same call, the same kernels and the
+ * same results, with the scratch memory taken from a static device array of the library
+ * (MIP_NOALLOC_SCRATCH_BYTES on every device it runs on, held until the process ends).
+ *
+ * No reference counterpart: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls no
+ * allocating routine. The array's device address is looked up on the first call on each device
+ * (the current device, which must own `stream`). A shape whose workspace
+ * (mip_paged_decode_workspace) exceeds MIP_NOALLOC_SCRATCH_BYTES returns MIP_E2BIG before
+ * anything is launched. Every call on one device shares that device's array, so calls that can
+ * run concurrently on one device (different streams, several host threads) race; calls ordered
+ * on one stream do not.
+ */
+#define MIP_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int mip_paged_decode_append_noalloc(const void* k_new, const void* v_new,
+                                    int64_t k_stride_tok, int64_t k_stride_head,
+                                    int64_t v_stride_tok, int64_t v_stride_head,
+                                    const int64_t* slot_mapping,
+                                    void* out, int64_t out_stride_b, int64_t out_stride_h,
+                                    const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                    void* k_cache, void* v_cache, int64_t num_cache_blocks,
+                                    const int32_t* block_tables, int64_t bt_stride,
+                                    const int32_t* context_lens,
+                                    int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
+                                    float scale, const void* plan, size_t plan_bytes, int32_t dtype,
+                                    void* stream);
 
 /*
  * Work plan of the decode kernels for one decode step (no reference counterpart: the

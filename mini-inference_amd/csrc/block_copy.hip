@@ -94,6 +94,7 @@ extern "C" const char* mip_status_string(int status) {
   switch (status) {
     case MIP_OK: return "ok";
     case MIP_EINVAL: return "invalid argument";
+    case MIP_E2BIG: return "the call needs more scratch than the library's static array holds";
     case MIP_EUNSUPPORTED: return "unsupported shape (no compiled kernel)";
     default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown status";
   }

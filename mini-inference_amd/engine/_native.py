@@ -13,7 +13,8 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libmipaged.so"
 
 MIP_F32, MIP_F16, MIP_BF16 = 0, 1, 2
-MIP_OK, MIP_EINVAL, MIP_EUNSUPPORTED = 0, -22, -95
+MIP_OK, MIP_E2BIG, MIP_EINVAL, MIP_EUNSUPPORTED = 0, -7, -22, -95
+MIP_NOALLOC_SCRATCH_BYTES = 32 << 20
 MIP_ALGO = {"auto": 0, "valu": 1, "mfma": 2, "stream": 3}
 
 EXPORTED = (
@@ -24,6 +25,7 @@ EXPORTED = (
     "mip_rope_kv_append",
     "mip_paged_decode",
     "mip_paged_decode_append",
+    "mip_paged_decode_append_noalloc",
     "mip_paged_decode_workspace",
     "mip_paged_decode_plan",
     "mip_paged_decode_plan_bytes",
@@ -60,6 +62,12 @@ _SIGNATURES = {
         [_vp, _vp, _i64, _i64, _i64, _i64, _vp,
          _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
          _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp, _sz, _i32, _vp],
+    ),
+    "mip_paged_decode_append_noalloc": (
+        _c.c_int,
+        [_vp, _vp, _i64, _i64, _i64, _i64, _vp,
+         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
+         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _i32, _vp],
     ),
     "mip_paged_decode_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "mip_paged_decode_plan_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
