@@ -1,0 +1,100 @@
+"""Write the allocator fixture (alloc_churn.json / alloc_churn.npz) from the reference's own
+allocator.
+
+    python tests/golden/make_alloc_golden.py
+
+Runs in the build container only: it imports ``engine.kv_cache.PagedKVCache`` from the
+reference checkout at /root/reference (pure Python over an OrderedDict; the pool tensors are
+made tiny: 1 layer, 1 kv head, head_dim 1, on the CPU). This build's allocator claims to hand
+out the same block ids as the reference's under any trace, and the reference's own tests pin
+that only on short traces (tests/test_kv_cache.py:163-175, :210-242), so this script records:
+
+* the 256 block tables of the bf16 B=256 workload (log-uniform contexts 128-4096, block 16,
+  32,768-block pool scrambled by 5,000 seeded alloc / grow / free events), driven by this
+  build's own workload code (``workloads.churn`` and ``workloads.context_lengths``, run
+  against the reference allocator exactly as ``build_decode_batch`` runs them against this
+  build's);
+* one digest per event of a 3,000-event prefix-caching trace (``alloc_trace.prefix_churn``).
+
+tests/test_host.py replays both on this build's allocator and compares. The fixture holds
+data only (block ids and digests).
+"""
+
+from __future__ import annotations
+
+import importlib
+import importlib.util
+import json
+import random
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent.parent
+REFERENCE = Path("/root/reference")
+sys.path.insert(0, str(HERE))
+
+import alloc_trace  # noqa: E402
+
+
+def this_builds_workloads():
+    """This build's engine package under the name ``mi_engine`` (the reference's is ``engine``)."""
+    pkg = ROOT / "mini-inference_amd" / "engine"
+    spec = importlib.util.spec_from_file_location("mi_engine", pkg / "__init__.py",
+                                                  submodule_search_locations=[str(pkg)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["mi_engine"] = mod
+    spec.loader.exec_module(mod)
+    return importlib.import_module("mi_engine.workloads")
+
+
+def reference_cache_class():
+    sys.path.insert(0, str(REFERENCE))
+    from engine.kv_cache import PagedKVCache  # the reference's allocator
+
+    return PagedKVCache
+
+
+def config3_tables(cache_cls, workloads) -> list[list[int]]:
+    """The allocator steps of build_decode_batch for the B=256 workload, on ``cache_cls``."""
+    shape = workloads.SHAPES[3]
+    ctx = workloads.context_lengths(shape, 0)
+    cache = cache_cls(1, 1, 1, shape.num_blocks, shape.block_size, max_seqs=max(shape.batch, 1024),
+                      max_len=max(max(ctx) + 1, 8192), dtype=torch.float16, device="cpu")
+    rng = random.Random(0 + 1)
+    workloads.churn(cache, shape.churn_events, rng, max_tokens=shape.ctx_hi)
+    tables = []
+    for n in ctx:
+        slot = cache.allocate(n + 1)
+        cache.lengths[slot] = n
+        tables.append(list(cache.block_tables[slot]))
+    return tables
+
+
+def main() -> None:
+    workloads = this_builds_workloads()
+    ref_cls = reference_cache_class()
+    tables = config3_tables(ref_cls, workloads)
+    pool = alloc_trace.PREFIX_POOL
+    cache = ref_cls(1, 1, 1, pool["num_blocks"], pool["block_size"], pool["max_seqs"], pool["max_len"],
+                    torch.float16, "cpu", enable_prefix_caching=True)
+    digests = alloc_trace.prefix_churn(cache)
+    lengths = np.asarray([len(t) for t in tables], dtype=np.int32)
+    flat = np.asarray([b for t in tables for b in t], dtype=np.int32)
+    np.savez_compressed(HERE / "alloc_churn.npz", table_lengths=lengths, table_blocks=flat)
+    meta = {
+        "source": "reference engine/kv_cache.py PagedKVCache (allocate / ensure_capacity / free / register_prefix)",
+        "config3": {"sequences": len(tables), "blocks": int(flat.size), "first_table": tables[0][:16]},
+        "prefix_trace": {"events": len(digests), "seed": alloc_trace.PREFIX_SEED, "pool": pool,
+                         "prefix_hit_tokens": cache.prefix_hit_tokens, "digests": digests},
+    }
+    (HERE / "alloc_churn.json").write_text(json.dumps(meta, indent=1) + "\n")
+    print(f"wrote {len(tables)} tables ({flat.size} blocks) and {len(digests)} trace digests; "
+          f"prefix hit tokens {cache.prefix_hit_tokens}")
+
+
+if __name__ == "__main__":
+    main()

@@ -95,6 +95,77 @@ def test_slot_ids_and_lru_reuse_order():
 # ----------------------------------------------------------------------------- decode context index math
 
 
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def _alloc_fixture():
+    import json
+    import sys
+
+    if str(GOLDEN) not in sys.path:
+        sys.path.insert(0, str(GOLDEN))
+    import alloc_trace
+
+    meta = json.loads((GOLDEN / "alloc_churn.json").read_text())
+    with np.load(GOLDEN / "alloc_churn.npz") as z:
+        lengths, flat = z["table_lengths"], z["table_blocks"]
+    tables = np.split(flat, np.cumsum(lengths)[:-1])
+    return alloc_trace, meta, [t.tolist() for t in tables]
+
+
+def _prefix_cache(cls=PagedKVCache):
+    import alloc_trace
+
+    pool = alloc_trace.PREFIX_POOL
+    return cls(1, 1, 1, pool["num_blocks"], pool["block_size"], pool["max_seqs"], pool["max_len"], torch.float16,
+               "cpu", enable_prefix_caching=True)
+
+
+def test_allocator_matches_reference_under_config3_churn():
+    """The bf16 B=256 workload's 256 block tables (after 5,000 seeded alloc / grow / free events
+    on a 32,768-block pool) equal the ones the reference allocator hands out for the same calls
+    (tests/golden/make_alloc_golden.py, engine/kv_cache.py:468-560)."""
+    import dataclasses
+
+    from engine import workloads
+
+    _, meta, want = _alloc_fixture()
+    shape = dataclasses.replace(workloads.SHAPES[3], num_layers=1, head_dim=8)  # same allocator calls, tiny pool
+    batch = workloads.build_decode_batch(shape, "cpu", seed=0, fill_pool=False)
+    got = [list(batch.cache.block_tables[s]) for s in batch.slots]
+    assert len(got) == meta["config3"]["sequences"] == 256
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert g == w, f"sequence {i}: first differing block at {next(j for j, (a, b) in enumerate(zip(g, w)) if a != b)}"
+
+
+def test_allocator_matches_reference_under_prefix_caching_trace():
+    """3,000 events of admissions with shared prompt prefixes (prefix hits), growth, preemption
+    and frees: every event's observation (slot, table, length, hit tokens, free blocks) equals
+    the reference allocator's, by digest."""
+    alloc_trace, meta, _ = _alloc_fixture()
+    cache = _prefix_cache()
+    got = alloc_trace.prefix_churn(cache)
+    want = meta["prefix_trace"]["digests"]
+    first = next((i for i, (g, w) in enumerate(zip(got, want)) if g != w), None)
+    assert first is None, f"first divergence at event {first}"
+    assert cache.prefix_hit_tokens == meta["prefix_trace"]["prefix_hit_tokens"] > 0
+
+
+def test_prefix_trace_catches_a_policy_change():
+    """The trace is sensitive to the reuse policy: an allocator that queues released blocks
+    without a cached prefix at the back (reused last), instead of the front, diverges."""
+    alloc_trace, meta, _ = _alloc_fixture()
+
+    class BackOfQueue(PagedKVCache):
+        def _release(self, block: int) -> None:
+            self._ref_counts[block] -= 1
+            if self._ref_counts[block] == 0:
+                self._free_blocks[block] = None
+
+    got = alloc_trace.prefix_churn(_prefix_cache(BackOfQueue))
+    assert got != meta["prefix_trace"]["digests"]
+
+
 def test_decode_context_matches_oracle_inputs():
     cache = tiny_paged(num_blocks=12, block_size=4)
     lengths = [6, 9, 3]
