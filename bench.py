@@ -296,7 +296,7 @@ def prefill_measure(dev, iters: int = 30) -> dict:
         "workload": f"packed prefill attention over a cached prefix: {len(pb.children)} forks of a "
                     f"{pb.prefix_len}-token prefix + suffixes U[32,512] ({n} new tokens), fp16, 14q/2kv heads d64, "
                     "block 16, one layer",
-        "kernel": "paged_prefill_kernel<f16, D=64, QR=8, NC=4>",
+        "kernel": "paged_prefill_kernel<f16, D=64, NC=4> (query rows packed as (token, head) pairs, 36 tokens per workgroup)",
         "us_per_layer": round(t * 1e6, 1),
         "bound": "mfma",
         "achieved": round(tflops, 1),

@@ -10,10 +10,11 @@
 // block-diagonal causal prefill of engine/kv_cache.py:290-294.
 //
 // Work split: an item is (kv head, sequence, block of TQ new tokens), done by a workgroup of
-// 4 wavefronts. The query rows of an item are (token, head of the kv head's group) pairs: a
-// 16-row column block holds 16 / QR tokens x QR head slots (the group's G heads, padded to
-// QR), and each wavefront owns NC column blocks. The grid is persistent and walks a
-// longest-first work list (paged_prefill_kernel).
+// 4 wavefronts owning NC 16-row column blocks each. The item's query rows are its (token,
+// head of the kv head's group) pairs, packed token-major with no padding: row r is head
+// r % G of token r / G, and TQ = 64 NC / G tokens fill all but 64 NC mod G rows (252 of 256
+// at G = 7). The grid is persistent and walks a longest-first work list
+// (paged_prefill_kernel).
 //
 // Per 32-key tile: all 256 threads copy the K and V rows (found through the block table) into
 // an LDS stage (two stages: the next tile's rows are fetched into registers while the current
@@ -64,7 +65,8 @@ struct PrefillArgs {
   const int32_t* cu_q;       // [S + 1] packed row offsets of each sequence's new tokens
   const int32_t* ctx_start;  // [S] tokens cached before this pass (position of token 0)
   int hkv, group, bs, log2_bs, max_blocks;
-  int num_seqs, zb;        // sequences; blocks of TQ new tokens the longest one can have
+  int tq;                  // new tokens per work item: query rows per item / group
+  int num_seqs, zb;        // sequences; blocks of tq new tokens the longest one can have
   float scale_log2;
 };
 
@@ -117,14 +119,13 @@ struct PShape {
 // smem holds the two K | V stages, s_ok[stage][key] whether a key row is a real key (valid
 // block id), byte w of s_wok[stage] whether every key row wavefront w loaded is. Called by
 // the whole workgroup (the barriers inside are workgroup-wide).
-template <int DT, int D, int QR, int NC>
+template <int DT, int D, int NC>
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int s, int blk, char* smem,
                                              uint8_t (*s_ok)[kKT], uint32_t* s_wok) {
   using P = PShape<D>;
   using Ops = MfmaOps<DT>;
   constexpr int RB = P::RB, CPR = P::CPR, KC = P::KC, MT = P::MT;
-  constexpr int TPC = 16 / QR;                 // tokens per column block
-  constexpr int TQ = kPW * NC * TPC;           // tokens per workgroup
+  const int TQ = a.tq;  // tokens per workgroup
 
   const int q0 = a.cu_q[s];
   const int n_s = a.cu_q[s + 1] - q0;
@@ -150,12 +151,15 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
   int wave_pmax = -1;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int tok = tok_lo + (w * NC + c) * TPC + i16 / QR;
-    const int g = i16 % QR;
-    live[c] = g < G && tok < tok_hi;
+    // Row r = 16 (NC w + c) + i16 of the item: head g = r % G of its token r / G.
+    const int r = (w * NC + c) * 16 + i16;
+    const int tr = r / G, g = r - tr * G;
+    const int tok = tok_lo + tr;
+    live[c] = tr < TQ && tok < tok_hi;
     const int p = start + tok;
     pos[c] = live[c] ? (p < cap - 1 ? p : cap - 1) : -1;
-    const int last_tok = tok_lo + (w * NC + c) * TPC + TPC - 1;
+    int last_tok = tok_lo + ((w * NC + c) * 16 + 15) / G;  // the block's last row's token
+    last_tok = last_tok < tok_lo + TQ - 1 ? last_tok : tok_lo + TQ - 1;
     const int wp = start + (last_tok < tok_hi - 1 ? last_tok : tok_hi - 1);
     wave_pmax = wp > wave_pmax ? wp : wave_pmax;
     const char* qrow = a.q + ((static_cast<int64_t>(q0) + (live[c] ? tok : 0)) * a.q_st +
@@ -390,8 +394,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
     const float lt = lacc[c][0];
     if (!live[c]) continue;
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    const int tok = tok_lo + (w * NC + c) * TPC + i16 / QR;
-    const int g = i16 % QR;
+    const int r = (w * NC + c) * 16 + i16;
+    const int tr = r / G, g = r - tr * G;
+    const int tok = tok_lo + tr;
     S* orow = reinterpret_cast<S*>(a.out) + (static_cast<int64_t>(q0) + tok) * a.out_st +
               static_cast<int64_t>(kvh * G + g) * a.out_sh;
 #pragma unroll
@@ -423,18 +428,18 @@ __device__ __forceinline__ int block_inclusive_scan(int x, int* s_wtot) {
 
 // Two wavefronts per SIMD is the occupancy the register file allows at these tile sizes;
 // saying so lets the compiler use up to 256 registers instead of spilling.
-template <int DT, int D, int QR, int NC, bool PERSIST>
+template <int DT, int D, int NC, bool PERSIST>
 __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_prefill_kernel(
     PrefillArgs a) {
   using P = PShape<D>;
-  constexpr int TQ = kPW * NC * (16 / QR);
+  const int TQ = a.tq;
   __shared__ __attribute__((aligned(16))) char smem[2 * P::STAGE];
   __shared__ uint8_t s_ok[2][kKT];
   __shared__ uint32_t s_wok[2];
   static_assert(kPW == 4, "one byte per wavefront in s_wok");
   if constexpr (!PERSIST) {
     // One workgroup per (kv head, sequence, block), blocks of a sequence latest first.
-    prefill_item<DT, D, QR, NC>(a, blockIdx.x, blockIdx.y, gridDim.z - 1 - blockIdx.z, smem, s_ok, s_wok);
+    prefill_item<DT, D, NC>(a, blockIdx.x, blockIdx.y, gridDim.z - 1 - blockIdx.z, smem, s_ok, s_wok);
   } else {
     __shared__ int s_nb[kMaxSeqs];          // blocks of sequence s
     __shared__ int s_seq[kMaxSeqs];         // sequences by blocks, descending
@@ -490,7 +495,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
       const int seq = __builtin_amdgcn_readfirstlane(s_seq[rem / a.hkv]);
       const int kvh = __builtin_amdgcn_readfirstlane(rem % a.hkv);
       const int blk = __builtin_amdgcn_readfirstlane(zb - 1 - lo);
-      prefill_item<DT, D, QR, NC>(a, kvh, seq, blk, smem, s_ok, s_wok);
+      prefill_item<DT, D, NC>(a, kvh, seq, blk, smem, s_ok, s_wok);
     }
   }
 }
@@ -498,47 +503,45 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
 template <int D> constexpr int kNC = MIP_PREFILL_NC > 0 ? MIP_PREFILL_NC : (D == 64 ? 4 : 2);
 
 // Workgroups of the persistent kernel that fit on the device at once (0 on error).
-template <int DT, int D, int QR, int NC>
+template <int DT, int D, int NC>
 int persistent_grid() {
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &per_cu, reinterpret_cast<const void*>(paged_prefill_kernel<DT, D, QR, NC, true>), kPW * kWave, 0) !=
+          &per_cu, reinterpret_cast<const void*>(paged_prefill_kernel<DT, D, NC, true>), kPW * kWave, 0) !=
       hipSuccess)
     return 0;
   return cus * (per_cu > 0 ? per_cu : 1);
 }
 
-template <int DT, int D, int QR>
+template <int DT, int D>
 int launch_shape(PrefillArgs a, int num_seqs, int max_q_len, hipStream_t s) {
   constexpr int NC = kNC<D>;
-  constexpr int TQ = kPW * NC * (16 / QR);
+  const int TQ = kPW * NC * 16 / a.group;  // group <= 16, so at least one token per item
   const int zb = (max_q_len + TQ - 1) / TQ;
+  a.tq = TQ;
   a.num_seqs = num_seqs;
   a.zb = zb;
   // Persistent grid over a longest-first work list where it fits in LDS: a grid with one
   // workgroup per (kv head, sequence, block) leaves most of the device idle when lengths vary,
   // since the workgroups past a sequence's end occupy the dispatcher.
-  static const int grid_cap = persistent_grid<DT, D, QR, NC>();
+  static const int grid_cap = persistent_grid<DT, D, NC>();
   const int64_t items = static_cast<int64_t>(a.hkv) * num_seqs * zb;
   if (grid_cap > 0 && num_seqs <= kMaxSeqs && zb <= kMaxLevels) {
     const int grid = static_cast<int>(items < grid_cap ? items : grid_cap);
-    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, QR, NC, true>), dim3(grid), dim3(kPW * kWave), 0, s, a);
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, NC, true>), dim3(grid), dim3(kPW * kWave), 0, s, a);
   } else {
     if (num_seqs > 65535 || zb > 65535) return MIP_EUNSUPPORTED;
-    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, QR, NC, false>), dim3(a.hkv, num_seqs, zb), dim3(kPW * kWave), 0,
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, NC, false>), dim3(a.hkv, num_seqs, zb), dim3(kPW * kWave), 0,
                        s, a);
   }
   return status_from_hip(hipGetLastError());
 }
 
 template <int DT>
-int launch_dt(const PrefillArgs& a, int d, int qr, int num_seqs, int max_q_len, hipStream_t s) {
-  if (d == 64) return qr == 8 ? launch_shape<DT, 64, 8>(a, num_seqs, max_q_len, s)
-                              : launch_shape<DT, 64, 16>(a, num_seqs, max_q_len, s);
-  return qr == 8 ? launch_shape<DT, 128, 8>(a, num_seqs, max_q_len, s)
-                 : launch_shape<DT, 128, 16>(a, num_seqs, max_q_len, s);
+int launch_dt(const PrefillArgs& a, int d, int num_seqs, int max_q_len, hipStream_t s) {
+  return d == 64 ? launch_shape<DT, 64>(a, num_seqs, max_q_len, s) : launch_shape<DT, 128>(a, num_seqs, max_q_len, s);
 }
 
 }  // namespace
@@ -601,8 +604,7 @@ extern "C" int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_
   a.log2_bs = ilog2_exact(block_size);
   a.max_blocks = max_blocks_per_seq;
   a.scale_log2 = scale * 1.4426950408889634f;
-  const int qr = group <= 8 ? 8 : 16;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == MIP_BF16) return prefill::launch_dt<MIP_BF16>(a, head_dim, qr, num_seqs, max_q_len, s);
-  return prefill::launch_dt<MIP_F16>(a, head_dim, qr, num_seqs, max_q_len, s);
+  if (dtype == MIP_BF16) return prefill::launch_dt<MIP_BF16>(a, head_dim, num_seqs, max_q_len, s);
+  return prefill::launch_dt<MIP_F16>(a, head_dim, num_seqs, max_q_len, s);
 }
