@@ -409,9 +409,11 @@ def hbm_ceiling(dev, nbytes: int, chunk: int = 2048, sets: int = 24, iters: int 
                 grids: tuple[int, ...] = (1024, 2048, 4096, 8192)) -> dict:
     """What this GPU streams for ``nbytes`` (one decode call's algorithmic bytes): the library's
     read probe (``mip_hbm_read_probe``) over randomly placed ``chunk``-byte chunks of a 4 GiB
-    buffer, as the paged pool is read, and over one contiguous run, cycling ``sets`` disjoint
-    chunk sets so nothing is served from the 256 MB last-level cache; the fastest of ``grids``
-    (workgroups of 256 threads) is reported. HIP events."""
+    buffer; over random chunks drawn from a window of twice the bytes, as one layer's K and V
+    pools are read (a window per set, each of its chunks used once); and over one contiguous
+    run. Each cycles ``sets`` disjoint chunk sets so nothing is served from the 256 MB
+    last-level cache; the fastest of ``grids`` (workgroups of 256 threads) is reported. HIP
+    events."""
     import torch
 
     from engine import _native
@@ -423,11 +425,19 @@ def hbm_ceiling(dev, nbytes: int, chunk: int = 2048, sets: int = 24, iters: int 
     per = nbytes // chunk
     gen = torch.Generator(device=dev).manual_seed(1)
     ids = torch.randperm(total, generator=gen, device=dev)[:per * sets].to(torch.int32).view(sets, per).contiguous()
+    # Windows of twice the bytes (one layer's K and V pools, about); the sets reuse the buffer's
+    # windows in turn, so a window comes back only after several others (far more than the
+    # last-level cache holds) have been read.
+    win = 2 * per
+    nwin = max(1, total // win)
+    windowed = [((i % nwin) * win + torch.randperm(win, generator=gen, device=dev)[:per]).to(torch.int32)
+                for i in range(sets)]
     seq = [torch.arange(i * per, (i + 1) * per, dtype=torch.int32, device=dev) for i in range(sets)]
     sink = torch.empty(max(grids) * 256, dtype=torch.int32, device=dev)
     st = torch.cuda.current_stream(dev).cuda_stream
     out = {}
-    for name, chunks in (("random_chunks", [ids[i] for i in range(sets)]), ("sequential", seq)):
+    for name, chunks in (("random_chunks", [ids[i] for i in range(sets)]), ("random_chunks_layer_window", windowed),
+                         ("sequential", seq)):
         by_grid = {}
         for grid in grids:
             args = [(buf.data_ptr(), pool_bytes, c.data_ptr(), per, chunk, sink.data_ptr(), grid, st) for c in chunks]
@@ -448,12 +458,13 @@ def hbm_ceiling(dev, nbytes: int, chunk: int = 2048, sets: int = 24, iters: int 
         out[name] = {"us": round(t * 1e6, 2), "GBps": round(per * chunk / t / 1e9, 1),
                      "frac": round(per * chunk / t / 1e9 / HBM_PEAK_GBPS, 4), "grid": grid,
                      "us_by_grid": {str(g): round(v * 1e6, 2) for g, v in by_grid.items()}}
-    del buf, ids, seq, sink
+    del buf, ids, windowed, seq, sink
     torch.cuda.empty_cache()
     out.update({"kernel": "hbm_read_probe_kernel", "bytes": per * chunk, "chunk_bytes": chunk,
-                "workload": f"read {per * chunk} B as {per} randomly placed {chunk}-byte chunks of a 4 GiB buffer "
-                            f"(and as one contiguous run), {sets} disjoint sets cycled, the fastest of grids "
-                            f"{list(grids)} x 256 threads"})
+                "workload": f"read {per * chunk} B as {per} randomly placed {chunk}-byte chunks of a 4 GiB buffer, "
+                            f"as {per} random chunks of a {win * chunk}-byte window (one per set), and as one "
+                            f"contiguous run; {sets} disjoint sets cycled, the fastest of grids {list(grids)} x 256 "
+                            f"threads"})
     return out
 
 
@@ -599,9 +610,12 @@ def main() -> int:
         try:
             hc = hbm_ceiling(dev, a_bytes + p_bytes)
             hc["decode_call_frac_of_random_chunks"] = round(achieved / hc["random_chunks"]["GBps"], 4)
+            hc["decode_call_frac_of_layer_window"] = round(achieved / hc["random_chunks_layer_window"]["GBps"], 4)
             result["hbm_ceiling"] = hc
             log(f"hbm probe: {hc['bytes']} B as random 2 KiB chunks {hc['random_chunks']['us']} us "
-                f"({hc['random_chunks']['GBps']} GB/s), sequential {hc['sequential']['us']} us "
+                f"({hc['random_chunks']['GBps']} GB/s), within a layer-sized window "
+                f"{hc['random_chunks_layer_window']['us']} us ({hc['random_chunks_layer_window']['GBps']} GB/s, the "
+                f"decode call reaches {hc['decode_call_frac_of_layer_window']:.1%} of it), sequential {hc['sequential']['us']} us "
                 f"({hc['sequential']['GBps']} GB/s); the decode call reaches "
                 f"{hc['decode_call_frac_of_random_chunks']:.1%} of the random-chunk rate")
         except Exception as exc:
