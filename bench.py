@@ -340,11 +340,13 @@ def append_measure(dev, iters: int = 40) -> dict:
     t = time_loop(call, iters)
     nbytes = 2 * (2 * n * hkv * d * 2) + 8 * n
     gbs = nbytes / t / 1e9
+    floor = copy_floor(dev, nbytes, sets=4)
     return {
         "workload": f"packed prefill append: {n} new tokens of {len(pb.children)} forks into one layer's pool, "
                     "fp16, 2 kv heads d64, block 16",
         "kernel": "kv_append_kernel",
         "us_per_layer": round(t * 1e6, 2),
+        "copy_floor_us": round(floor * 1e6, 2),
         "bound": "hbm",
         "achieved": round(gbs, 1),
         "peak": 8000.0,
@@ -352,6 +354,30 @@ def append_measure(dev, iters: int = 40) -> dict:
         "frac": round(gbs / 8000.0, 4),
         "bytes": nbytes,
     }
+
+
+def copy_floor(dev, nbytes: int, sets: int, iters: int = 40) -> float:
+    """Seconds a plain device copy (``torch.Tensor.copy_``) takes to move ``nbytes`` of traffic
+    (half read, half written) in one launch, cycling ``sets`` disjoint buffer pairs as the
+    measurement it is set beside does: the floor for a data-movement kernel of that size."""
+    import torch
+
+    half = nbytes // 2
+    pairs = [(torch.empty(half, dtype=torch.uint8, device=dev), torch.empty(half, dtype=torch.uint8, device=dev))
+             for _ in range(sets)]
+    it = [0]
+
+    def call():
+        src, dst = pairs[it[0] % sets]
+        dst.copy_(src)
+        it[0] += 1
+
+    for _ in range(sets):
+        call()
+    torch.cuda.synchronize()
+    t = time_loop(call, iters)
+    del pairs
+    return t
 
 
 def copy_measure(dev, iters: int = 40, sets: int = 8) -> dict:
@@ -391,11 +417,13 @@ def copy_measure(dev, iters: int = 40, sets: int = 8) -> dict:
     t = time_loop(call, iters)
     nbytes = 2 * pairs_per * layers * 2 * hkv * bs * d * 2
     gbs = nbytes / t / 1e9
+    floor = copy_floor(dev, nbytes, sets=sets)
     return {
         "workload": f"copy-on-write of {pairs_per} partially filled shared blocks (one per fork), {layers} layers, "
                     "K and V, fp16, 2 kv heads d64, block 16",
         "kernel": "copy_blocks_kernel<16>",
         "us": round(t * 1e6, 2),
+        "copy_floor_us": round(floor * 1e6, 2),
         "bound": "hbm",
         "achieved": round(gbs, 1),
         "peak": 8000.0,
@@ -653,14 +681,16 @@ def main() -> int:
         try:
             result["packed_append"] = append_measure(dev)
             pa = result["packed_append"]
-            log(f"packed append: {pa['us_per_layer']} us/layer, {pa['achieved']} GB/s ({pa['frac']:.1%} of peak)")
+            log(f"packed append: {pa['us_per_layer']} us/layer, {pa['achieved']} GB/s ({pa['frac']:.1%} of peak); "
+                f"a device copy of the same bytes takes {pa['copy_floor_us']} us")
         except Exception as exc:
             log(f"packed append measurement failed: {exc!r}")
             result["packed_append"] = None
         try:
             result["block_copy"] = copy_measure(dev)
             bc = result["block_copy"]
-            log(f"block copy: {bc['us']} us, {bc['achieved']} GB/s ({bc['frac']:.1%} of peak)")
+            log(f"block copy: {bc['us']} us, {bc['achieved']} GB/s ({bc['frac']:.1%} of peak); "
+                f"a device copy of the same bytes takes {bc['copy_floor_us']} us")
         except Exception as exc:
             log(f"block copy measurement failed: {exc!r}")
             result["block_copy"] = None
