@@ -19,7 +19,10 @@ Reported (one JSON line on stdout):
   decode_tok_s  B / full decode-step time of a random-init Qwen2.5-0.5B (embedding, 24 layers
                 with GEMMs, RoPE + append (one fused kernel, mip_rope_kv_append), attention,
                 MLP, final norm, logits), the step replayed as one captured HIP graph
-                (engine/cuda_graphs.py); decode_tok_s_eager: the same step launched eagerly
+                (engine/cuda_graphs.py); decode_tok_s_eager: the same step launched eagerly;
+                decode_tok_s_attend / decode_tok_s_eager_attend: the same two through the
+                reference's call protocol (the model applies apply_rope, then calls
+                ctx.attend, which appends and attends in one mip_paged_decode_append)
   prefill       packed prefill attention over a cached prefix (64 forks of a 520-token prefix,
                 suffixes U[32, 512], fp16): time per layer and TFLOP/s against the fp16 MFMA peak
   long_context  the same append + attention step at 28 query / 4 KV heads, head_dim 128, bf16,
@@ -209,9 +212,13 @@ def long_context_measure(dev, steps: int = 10) -> dict:
 def decode_tok_s(batch, steps: int, warmup: int) -> dict:
     """Full random-init Qwen2.5-0.5B decode step at this batch: eager, and replayed as one HIP graph.
 
-    A step = host tables + H2D, embedding, 24 layers (GEMMs, RoPE fused with the KV append,
-    paged attention, MLP), final norm and logits, synchronised. Sequence lengths are restored after
-    every step, so each step appends at the same positions and attends the same contexts.
+    A step = host tables + H2D, embedding, 24 layers (GEMMs, RoPE, KV append, paged attention,
+    MLP), final norm and logits, synchronised. Each is timed twice: with the RoPE fused into
+    the append (the contexts' default ``fuse_rope``), and through the reference's own call
+    protocol (the model applies ``apply_rope`` and calls ``ctx.attend(layer_idx, q, k, v)``,
+    engine/model.py:249-250), which a drop-in caller runs unchanged. Sequence lengths are
+    restored after every step, so each step appends at the same positions and attends the
+    same contexts.
     """
     import torch
 
@@ -227,22 +234,27 @@ def decode_tok_s(batch, steps: int, warmup: int) -> dict:
     tokens = torch.randint(0, cfg.vocab_size, (len(batch.slots),), generator=torch.Generator().manual_seed(5))
     ids = tokens.to(dev).unsqueeze(1)
     lengths = {s: cache.lengths[s] for s in batch.slots}
-
-    @torch.inference_mode()
-    def eager_step():
-        ctx = cache.decode_context(batch.slots)  # host tables + H2D, as the runner does each step
-        hidden = model(ids, ctx.positions.unsqueeze(1), ctx)
-        return model.compute_logits(hidden[:, -1]).float()
-
-    graphed = GraphedDecoder(model, cache, max_batch=len(batch.slots))
-    graphed.capture(batches=[len(batch.slots)])
     token_list = tokens.tolist()
 
-    @torch.inference_mode()
-    def graph_step():
-        out = graphed.decode(batch.slots, token_list)
-        cache.lengths.update(lengths)
-        return out
+    def eager(fuse_rope: bool):
+        @torch.inference_mode()
+        def step():
+            ctx = cache.decode_context(batch.slots)  # host tables + H2D, as the runner does each step
+            ctx.fuse_rope = fuse_rope
+            hidden = model(ids, ctx.positions.unsqueeze(1), ctx)
+            return model.compute_logits(hidden[:, -1]).float()
+        return step
+
+    def graphed(fuse_rope: bool):
+        dec = GraphedDecoder(model, cache, max_batch=len(batch.slots), fuse_rope=fuse_rope)
+        dec.capture(batches=[len(batch.slots)])
+
+        @torch.inference_mode()
+        def step():
+            out = dec.decode(batch.slots, token_list)
+            cache.lengths.update(lengths)
+            return out
+        return step
 
     def timed(fn):
         for _ in range(warmup):
@@ -256,11 +268,15 @@ def decode_tok_s(batch, steps: int, warmup: int) -> dict:
             times.append(time.perf_counter() - t0)
         return statistics.median(times)
 
-    t_eager = timed(eager_step)
-    t_graph = timed(graph_step)
+    t_eager = timed(eager(True))
+    t_graph = timed(graphed(True))
+    t_eager_attend = timed(eager(False))
+    t_graph_attend = timed(graphed(False))
     n = len(batch.slots)
     return {"tok_s": n / t_graph, "ms_per_step": t_graph * 1e3, "eager_tok_s": n / t_eager,
-            "eager_ms_per_step": t_eager * 1e3, "steps": steps}
+            "eager_ms_per_step": t_eager * 1e3, "attend_tok_s": n / t_graph_attend,
+            "attend_ms_per_step": t_graph_attend * 1e3, "eager_attend_tok_s": n / t_eager_attend,
+            "eager_attend_ms_per_step": t_eager_attend * 1e3, "steps": steps}
 
 
 def prefill_measure(dev, iters: int = 30) -> dict:
@@ -513,6 +529,7 @@ def small_batch_decode(dev, steps: int, warmup: int) -> dict:
                     "tables permuted over 16384 blocks",
         "tok_s": round(dm["tok_s"], 1), "ms_per_step": round(dm["ms_per_step"], 3),
         "eager_tok_s": round(dm["eager_tok_s"], 1), "eager_ms_per_step": round(dm["eager_ms_per_step"], 3),
+        "attend_tok_s": round(dm["attend_tok_s"], 1), "eager_attend_tok_s": round(dm["eager_attend_tok_s"], 1),
     }
 
 
@@ -656,8 +673,13 @@ def main() -> int:
             result["decode_tok_s"] = round(dm["tok_s"], 1)
             result["decode_ms_per_step"] = round(dm["ms_per_step"], 3)
             result["decode_tok_s_eager"] = round(dm["eager_tok_s"], 1)
-            log(f"full-model decode: graph {dm['ms_per_step']:.2f} ms/step ({dm['tok_s']:.0f} tok/s), "
-                f"eager {dm['eager_ms_per_step']:.2f} ms/step ({dm['eager_tok_s']:.0f} tok/s)")
+            result["decode_tok_s_attend"] = round(dm["attend_tok_s"], 1)
+            result["decode_tok_s_eager_attend"] = round(dm["eager_attend_tok_s"], 1)
+            log(f"full-model decode, RoPE fused into the append: graph {dm['ms_per_step']:.2f} ms/step "
+                f"({dm['tok_s']:.0f} tok/s), eager {dm['eager_ms_per_step']:.2f} ms/step ({dm['eager_tok_s']:.0f} tok/s)")
+            log(f"full-model decode, reference protocol (apply_rope + ctx.attend): graph "
+                f"{dm['attend_ms_per_step']:.2f} ms/step ({dm['attend_tok_s']:.0f} tok/s), eager "
+                f"{dm['eager_attend_ms_per_step']:.2f} ms/step ({dm['eager_attend_tok_s']:.0f} tok/s)")
         except Exception as exc:  # the headline kernel numbers stand on their own
             log(f"full-model decode failed: {exc!r}")
             result["decode_tok_s"] = None

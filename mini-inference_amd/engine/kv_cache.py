@@ -409,6 +409,7 @@ class PagedDecodeContext:
         self.scale = 1.0 / (cache.head_dim ** 0.5)
         self._mask: torch.Tensor | None = None
         self._plan: tuple[tuple, torch.Tensor | None] | None = None  # (shape key, work plan)
+        self._calls: paged_ops.DecodeStepCalls | None = None
 
     @property
     def tables(self) -> torch.Tensor:
@@ -443,13 +444,18 @@ class PagedDecodeContext:
             self._plan = (key, p)
         return self._plan[1]
 
+    @property
+    def calls(self) -> paged_ops.DecodeStepCalls:
+        """The step's layer calls: the shared arguments are checked on the first layer only."""
+        if self._calls is None:
+            self._calls = paged_ops.DecodeStepCalls(self.block_tables, self.context_lens, self.slot_mapping,
+                                                    self.scale, self.num_blocks, self.plan)
+        return self._calls
+
     def attend(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         """Append this step's k/v and attend (engine/kv_cache.py:611-620) in one fused call."""
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
-        out = paged_ops.paged_decode_append(q[:, :, 0], k[:, :, 0], v[:, :, 0], k_layer, v_layer, self.slot_mapping,
-                                            self.block_tables, self.context_lens, scale=self.scale,
-                                            max_blocks=self.num_blocks, plan=self.plan(q.shape[1], q.dtype))
-        return out.unsqueeze(2)
+        return self.calls.decode_append(q[:, :, 0], k[:, :, 0], v[:, :, 0], k_layer, v_layer).unsqueeze(2)
 
     def attend_rope(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
                     sin: torch.Tensor) -> torch.Tensor:
@@ -461,11 +467,8 @@ class PagedDecodeContext:
         """
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
         q1 = q[:, :, 0]
-        paged_ops.rope_kv_append(q1, k[:, :, 0], v[:, :, 0], cos[:, 0, 0], sin[:, 0, 0], k_layer, v_layer,
-                                 self.slot_mapping)
-        out = paged_ops.paged_decode(q1, k_layer, v_layer, self.block_tables, self.context_lens, scale=self.scale,
-                                     max_blocks=self.num_blocks, plan=self.plan(q.shape[1], q.dtype))
-        return out.unsqueeze(2)
+        self.calls.rope_append(q1, k[:, :, 0], v[:, :, 0], cos[:, 0, 0], sin[:, 0, 0], k_layer, v_layer)
+        return self.calls.decode(q1, k_layer, v_layer).unsqueeze(2)
 
     def commit(self) -> None:
         for s in self.slots:

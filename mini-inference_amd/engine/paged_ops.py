@@ -32,7 +32,13 @@ def _require_device(*tensors: torch.Tensor) -> None:
             )
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_ptr(device: torch.device) -> int:
+    """Handle of the current stream on ``device`` (``torch.cuda.current_stream(device).cuda_stream``)."""
+    if _raw_stream is not None and device.index is not None:
+        return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -133,11 +139,15 @@ def prepare_rope_kv_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Ten
     lib = _native.load()
     hq = 0 if q is None else q.shape[1]
     qp, qs0, qs1 = (None, 0, 0) if q is None else (q.data_ptr(), q.stride(0), q.stride(1))
+    # Positions of the per-call addresses are _ROPE_SLOTS (q, k, v, cos, sin, k_cache, v_cache).
     args = (qp, qs0, qs1, k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
             cos.data_ptr(), sin.data_ptr(), cos.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), nb,
             slot_mapping.data_ptr(), n, hq, hkv, d, bs, dtype_code(dt), _stream_ptr(k_cache.device))
     return PreparedCall(lib.mip_rope_kv_append, args, "mip_rope_kv_append",
                         (q, k, v, cos, sin, k_cache, v_cache, slot_mapping))
+
+
+_ROPE_SLOTS = (0, 3, 6, 9, 10, 12, 13)
 
 
 def rope_kv_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
@@ -253,6 +263,8 @@ def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
             raise ValueError(f"the plan was made for shape {made_for}, not this call's {want}")
     plan_ptr = plan.data_ptr() if plan is not None else None
     plan_bytes = plan.numel() * 4 if plan is not None else 0
+    # Positions of the per-call addresses are _DECODE_SLOTS (out, q, k_cache, v_cache), and
+    # _APPEND_SLOTS (k, v, out, q, k_cache, v_cache) in the fused tuple below.
     args = (out.data_ptr(), out.stride(0), out.stride(1), q.data_ptr(), q.stride(0), q.stride(1),
             k_cache.data_ptr(), v_cache.data_ptr(), nb, block_tables.data_ptr(), block_tables.stride(0),
             context_lens.data_ptr(), b, hq, hkv, d, bs, mb, scale, ws_ptr, ws_bytes, plan_ptr, plan_bytes, code,
@@ -273,6 +285,89 @@ def prepare_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
     fused = (k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1), slot_mapping.data_ptr(),
              *args)
     return PreparedCall(lib.mip_paged_decode_append, fused, "mip_paged_decode_append", keep + (k, v, slot_mapping)), out
+
+
+_DECODE_SLOTS = (0, 3, 6, 7)
+_APPEND_SLOTS = (0, 1, 7, 10, 13, 14)
+
+
+def _layout(t: torch.Tensor) -> tuple:
+    return (t.shape, t.stride(), t.dtype, t.device)
+
+
+class DecodeStepCalls:
+    """The per-layer calls of one decode step, with the step's fixed arguments checked once.
+
+    Within a step every layer's call takes the same block tables, context lengths, slot
+    mapping, plan and workspace; only q, k, v, the layer's pool and the output change, and
+    they keep one layout. Each method runs the full checks of :func:`prepare_paged_decode` /
+    :func:`prepare_rope_kv_append` when the layout of its tensors (shapes, strides, dtypes,
+    devices) differs from the call before, and otherwise issues the same C-ABI call with
+    the new addresses and the current stream. ``plan`` maps (num_heads, dtype) to the step's
+    work plan (or None).
+    """
+
+    def __init__(self, block_tables: torch.Tensor, context_lens: torch.Tensor, slot_mapping: torch.Tensor,
+                 scale: float, max_blocks: int, plan) -> None:
+        self.block_tables, self.context_lens, self.slot_mapping = block_tables, context_lens, slot_mapping
+        self.scale, self.max_blocks, self._plan = scale, max_blocks, plan
+        self._cached: dict[str, tuple] = {}  # kind -> (layout key, fn, argument list, kept tensors)
+
+    def _issue(self, kind: str, key: tuple, prepare, ptrs: tuple, slots: tuple, device: torch.device) -> None:
+        hit = self._cached.get(kind)
+        if hit is None or hit[0] != key:
+            call = prepare()
+            if call is _noop:
+                return
+            self._cached[kind] = (key, call._fn, list(call._args), call.keep)
+            call()
+            return
+        _, fn, args, _ = hit
+        for i, p in zip(slots, ptrs):
+            args[i] = p
+        args[-1] = _stream_ptr(device)
+        st = fn(*args)
+        if st:
+            _native.check(st, fn.__name__)
+
+    def decode_append(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                      v_cache: torch.Tensor) -> torch.Tensor:
+        """:func:`paged_decode_append` of one layer; returns ``out [B, Hq, D]``."""
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        key = (_layout(q), _layout(k), _layout(v), _layout(k_cache), _layout(v_cache))
+
+        def prepare():
+            return prepare_paged_decode(q, k_cache, v_cache, self.block_tables, self.context_lens, self.scale, out,
+                                        self.max_blocks, append=(k, v, self.slot_mapping),
+                                        plan=self._plan(q.shape[1], q.dtype))[0]
+
+        self._issue("append", key, prepare, (k.data_ptr(), v.data_ptr(), out.data_ptr(), q.data_ptr(),
+                                             k_cache.data_ptr(), v_cache.data_ptr()), _APPEND_SLOTS, q.device)
+        return out
+
+    def decode(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> torch.Tensor:
+        """:func:`paged_decode` of one layer; returns ``out [B, Hq, D]``."""
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        key = (_layout(q), _layout(k_cache), _layout(v_cache))
+
+        def prepare():
+            return prepare_paged_decode(q, k_cache, v_cache, self.block_tables, self.context_lens, self.scale, out,
+                                        self.max_blocks, plan=self._plan(q.shape[1], q.dtype))[0]
+
+        self._issue("decode", key, prepare, (out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr()),
+                    _DECODE_SLOTS, q.device)
+        return out
+
+    def rope_append(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                    k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+        """:func:`rope_kv_append` of one layer (q and k rotated in place)."""
+        key = (_layout(q), _layout(k), _layout(v), _layout(cos), _layout(sin), _layout(k_cache), _layout(v_cache))
+
+        def prepare():
+            return prepare_rope_kv_append(q, k, v, cos, sin, k_cache, v_cache, self.slot_mapping)
+
+        self._issue("rope", key, prepare, (q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                           k_cache.data_ptr(), v_cache.data_ptr()), _ROPE_SLOTS, k.device)
 
 
 def prepare_decode_plan(context_lens: torch.Tensor, block_tables: torch.Tensor, num_heads: int, num_kv_heads: int,

@@ -771,3 +771,91 @@ def test_eager_decode_context_device_tables_match_oracle(gpu):
         assert err <= TOL["bfloat16"], f"step {step}: {err}"
         ctx.commit()
     assert cache.cow_copies >= 1
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@torch.inference_mode()
+def test_decode_context_layer_calls_equal_checked_calls(gpu, dtype):
+    """PagedDecodeContext checks the step's shared arguments on its first layer call and then
+    only swaps addresses (paged_ops.DecodeStepCalls). Over 4 layers, with a q layout change at
+    layer 2 (re-checked) and back at layer 3, and one layer issued on a side stream, both
+    protocols (attend; attend_rope) give outputs and pools bit-equal to the fully checked
+    paged_ops calls on the same inputs."""
+    from engine import paged_ops
+    from engine.kv_cache import PagedKVCache
+    from engine.model import rope_cos_sin
+
+    announce(f"decode context layer calls vs checked calls, {dtype}")
+    dt = DTYPES[dtype]
+    lengths = [13, 30, 47, 5, 62, 16, 31, 100]
+    cache = PagedKVCache(4, 2, 64, num_blocks=160, block_size=16, max_seqs=16, max_len=512, dtype=dt, device=gpu)
+    slots = []
+    for n in lengths:
+        s = cache.allocate(n + 1)
+        cache.lengths[s] = n
+        slots.append(s)
+    gen = torch.Generator(device=gpu).manual_seed(7)
+    cache.k.normal_(0.0, 1.0, generator=gen)
+    cache.v.normal_(0.0, 1.0, generator=gen)
+    k0, v0 = cache.k.clone(), cache.v.clone()
+    b = len(slots)
+    qs = [torch.randn(b, 14, 1, 64, generator=gen, device=gpu).to(dt) for _ in range(4)]
+    qs[2] = torch.randn(b, 14, 1, 128, generator=gen, device=gpu).to(dt)[..., :64]  # other strides
+    ks = [torch.randn(b, 2, 1, 64, generator=gen, device=gpu).to(dt) for _ in range(4)]
+    vs = [torch.randn(b, 2, 1, 64, generator=gen, device=gpu).to(dt) for _ in range(4)]
+    side = torch.cuda.Stream(device=gpu)
+    assert paged_ops._stream_ptr(gpu) == torch.cuda.current_stream(gpu).cuda_stream
+    with torch.cuda.stream(side):
+        assert paged_ops._stream_ptr(gpu) == side.cuda_stream
+
+    def run_context(rope: bool):
+        cache.k.copy_(k0)
+        cache.v.copy_(v0)
+        ctx = cache.decode_context(slots)
+        cos, sin = rope_cos_sin(ctx.positions.unsqueeze(1), 64, 1e6, dt)
+        outs = []
+        for layer in range(4):
+            q, k, v = qs[layer].clone(), ks[layer].clone(), vs[layer].clone()
+            if layer == 2:  # keep the wider strides of this layer's q (clone() would compact them)
+                q = torch.empty_strided(qs[2].shape, qs[2].stride(), dtype=dt, device=gpu).copy_(qs[2])
+            if layer == 1:
+                side.wait_stream(torch.cuda.current_stream(gpu))
+                with torch.cuda.stream(side):
+                    out = ctx.attend_rope(layer, q, k, v, cos, sin) if rope else ctx.attend(layer, q, k, v)
+                torch.cuda.current_stream(gpu).wait_stream(side)
+            else:
+                out = ctx.attend_rope(layer, q, k, v, cos, sin) if rope else ctx.attend(layer, q, k, v)
+            outs.append(out[:, :, 0].clone())
+        torch.cuda.synchronize()
+        return ctx, cos, sin, outs, cache.k.clone(), cache.v.clone()
+
+    def run_checked(ctx, cos, sin, rope: bool):
+        cache.k.copy_(k0)
+        cache.v.copy_(v0)
+        plan = ctx.plan(14, dt)
+        outs = []
+        for layer in range(4):
+            q = torch.empty_strided(qs[layer].shape, qs[layer].stride(), dtype=dt, device=gpu).copy_(qs[layer])
+            k, v = ks[layer].clone(), vs[layer].clone()
+            kl, vl = cache.k[layer], cache.v[layer]
+            if rope:
+                paged_ops.rope_kv_append(q[:, :, 0], k[:, :, 0], v[:, :, 0], cos[:, 0, 0], sin[:, 0, 0], kl, vl,
+                                         ctx.slot_mapping)
+                out = paged_ops.paged_decode(q[:, :, 0], kl, vl, ctx.block_tables, ctx.context_lens, scale=ctx.scale,
+                                             max_blocks=ctx.num_blocks, plan=plan)
+            else:
+                out = paged_ops.paged_decode_append(q[:, :, 0], k[:, :, 0], v[:, :, 0], kl, vl, ctx.slot_mapping,
+                                                    ctx.block_tables, ctx.context_lens, scale=ctx.scale,
+                                                    max_blocks=ctx.num_blocks, plan=plan)
+            outs.append(out.clone())
+        torch.cuda.synchronize()
+        return outs, cache.k.clone(), cache.v.clone()
+
+    for rope in (False, True):
+        ctx, cos, sin, got, kg, vg = run_context(rope)
+        assert ctx.calls._cached, "the layer calls went through the step's call cache"
+        want, kw, vw = run_checked(ctx, cos, sin, rope)
+        for layer in range(4):
+            assert torch.equal(got[layer], want[layer]), f"rope={rope} layer {layer}: output"
+        assert torch.equal(kg, kw) and torch.equal(vg, vw), f"rope={rope}: pools"
+        assert not torch.equal(kg, k0), "the calls appended"
