@@ -54,7 +54,9 @@ int mip_version(void);
  * Decode attention algorithm (no reference counterpart: the reference has one path, SDPA).
  * MIP_ALGO_AUTO picks per shape: the stream-K MFMA kernel for 16-bit K/V at head_dim 64/128
  * (batch <= 4096), else the per-partition MFMA kernel, else the VALU kernel (fp32, other head
- * sizes). A forced algorithm applies only where its kernel exists for the shape. The setting is
+ * sizes; a query group of more than 8 heads is split over workgroups of at most 8, each of
+ * which reads the kv head's keys and values). A forced algorithm applies only where its kernel
+ * exists for the shape (the MFMA kernels: group <= 16). The setting is
  * process-wide, starts from the MIP_DECODE_ALGO environment variable (valu | mfma | stream,
  * read once), and is meant for kernel comparisons and tests; it must not change while decode
  * calls are being enqueued, since the workspace and plan sizes depend on it. Returns the
@@ -280,10 +282,11 @@ int mip_paged_decode_plan(const int32_t* context_lens, const int32_t* block_tabl
  * depends on the integer arguments alone.
  *
  * Kernels: 16-bit dtypes at head_dim 64 or 128 with group <= 16 run the MFMA prefill kernel
- * (q rows 16-byte aligned, out rows 8-byte aligned). Every other shape with group <= 8 and
- * head_dim a power of two in 8 .. 256 (fp32 included) runs the VALU decode kernel, one
- * workgroup per (new token, kv head) over that token's keys (q rows 4-byte aligned); the
- * grid then has num_seqs * max_q_len workgroups per kv head. Other shapes: MIP_EUNSUPPORTED.
+ * (q rows 16-byte aligned, out rows 8-byte aligned). Every other shape with head_dim a power
+ * of two in 8 .. 256 (fp32 included) runs the VALU decode kernel, one workgroup per (new
+ * token, kv head, group of at most 8 of its query heads) over that token's keys (q rows
+ * 4-byte aligned); the grid then has num_seqs * max_q_len workgroups per such group. Other
+ * shapes: MIP_EUNSUPPORTED.
  */
 int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_stride_head,
                       const void* q, int64_t q_stride_tok, int64_t q_stride_head,

@@ -152,10 +152,12 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_part(DecodeArgs a) {
   __shared__ float sh_l[kNW][G];
   __shared__ float sh_acc[kNW][G][D];
 
-  const int kvh = blockIdx.y;
+  // Query heads h0 .. h0 + G - 1 of kv head kvh (a group of more than 8 heads is split over
+  // a.gsplit workgroups, each holding G of them in registers).
+  const int kvh = a.gsplit > 1 ? static_cast<int>(blockIdx.y) / a.gsplit : static_cast<int>(blockIdx.y);
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int h0 = kvh * G;
+  const int h0 = static_cast<int>(blockIdx.y) * G;
 
   // Decode: (partition, kv head, sequence). Packed prefill: (sequence x new token, kv head),
   // one partition; the row's keys are its sequence's keys up to its own position.
@@ -629,18 +631,19 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_part_mfma(DecodeArgs
   }
 }
 
-// Combine the partitions of every sequence that needed more than one. Grid (kv heads, batch).
+// Combine the partitions of every sequence that needed more than one. Grid (groups of G query
+// heads, batch): kv heads, or kv heads x a.gsplit for a split VALU group.
 template <int DT, int D, int G>
 __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
   using S = typename Elem<DT>::S;
-  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int hg = blockIdx.x, b = blockIdx.y;
   int ctx = a.lens[b];
   const int cap = a.max_blocks * a.bs;
   ctx = ctx < cap ? ctx : cap;
   const int np_b = ctx > 0 ? (ctx + a.part_tokens - 1) / a.part_tokens : 1;
   if (np_b <= 1) return;
   S* out_base = reinterpret_cast<S*>(a.out);
-  const int h0 = kvh * G;
+  const int h0 = hg * G;
   for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
     const int g = i / D, d = i % D;
     const int64_t slot0 = (static_cast<int64_t>(b) * a.hq + h0 + g) * a.nparts;
@@ -687,7 +690,7 @@ Algo choose_algo(int dtype, int d, int g, int batch) {
   const int f = forced_algo().load(std::memory_order_relaxed);
   const bool mfma_ok = mfma_eligible(dtype, d, g);
   const bool stream_ok = mfma_ok && stream_config(dtype, d, g, batch).ok;
-  if (f == MIP_ALGO_VALU && g <= 8) return Algo::kValu;
+  if (f == MIP_ALGO_VALU) return Algo::kValu;
   if (f == MIP_ALGO_MFMA && mfma_ok) return Algo::kMfma;
   if (f == MIP_ALGO_STREAM && stream_ok) return Algo::kStream;
   return stream_ok ? Algo::kStream : mfma_ok ? Algo::kMfma : Algo::kValu;
@@ -749,6 +752,16 @@ WsLayout ws_layout(int batch, int hq, int hkv, int d, int bs, int max_blocks, in
   w.acc_off = align_up(static_cast<int64_t>(batch) * hq * w.nparts * 2 * 4, 256);
   w.bytes = w.acc_off + align_up(static_cast<int64_t>(batch) * hq * w.nparts * d * 4, 256);
   return w;
+}
+
+// Workgroups per kv head of the VALU kernel: the smallest divisor of the query group that
+// leaves at most 8 query heads per workgroup (a workgroup keeps q, the running maxima and sums
+// and the accumulators of all its heads in registers). Each of them reads the kv head's keys
+// and values, so the K/V traffic grows by this factor.
+int valu_split(int g) {
+  for (int s = (g + 7) / 8; s < g; ++s)
+    if (g % s == 0) return s;
+  return g > 1 ? g : 1;
 }
 
 using KernelFn = void (*)(DecodeArgs);
@@ -854,8 +867,8 @@ int valu_prefill_launch(void* out, int64_t out_stride_tok, int64_t out_stride_he
                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
                         float scale, int32_t dtype, hipStream_t stream) {
   const int group = num_heads / num_kv_heads;
-  if (group > 8) return MIP_EUNSUPPORTED;
-  const KernelPair kp = pick_kernel(Algo::kValu, dtype, head_dim, group);
+  const int vsplit = valu_split(group);
+  const KernelPair kp = pick_kernel(Algo::kValu, dtype, head_dim, group / vsplit);
   if (!kp.part) return MIP_EUNSUPPORTED;
   const int64_t es = dtype == MIP_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return MIP_EINVAL;
@@ -870,7 +883,7 @@ int valu_prefill_launch(void* out, int64_t out_stride_tok, int64_t out_stride_he
   if (cap >= (int64_t{1} << 30)) return MIP_EINVAL;
   if (num_cache_blocks * num_kv_heads * block_size >= (int64_t{1} << 31)) return MIP_EINVAL;
   const int64_t grid_x = static_cast<int64_t>(num_seqs) * max_q_len;
-  if (grid_x >= (int64_t{1} << 31) || num_kv_heads > 65535) return MIP_EUNSUPPORTED;
+  if (grid_x >= (int64_t{1} << 31) || static_cast<int64_t>(num_kv_heads) * vsplit > 65535) return MIP_EUNSUPPORTED;
   DecodeArgs a{};
   a.out = static_cast<char*>(out);
   a.out_sb = out_stride_tok;
@@ -895,7 +908,9 @@ int valu_prefill_launch(void* out, int64_t out_stride_tok, int64_t out_stride_he
   a.cu_q = cu_q;
   a.ctx_start = ctx_start;
   a.max_q_len = max_q_len;
-  hipLaunchKernelGGL(kp.part, dim3(static_cast<unsigned>(grid_x), num_kv_heads, 1), dim3(kNW * kWave), 0, stream, a);
+  a.gsplit = vsplit;
+  hipLaunchKernelGGL(kp.part, dim3(static_cast<unsigned>(grid_x), num_kv_heads * vsplit, 1), dim3(kNW * kWave), 0,
+                     stream, a);
   return status_from_hip(hipGetLastError());
 }
 
@@ -940,7 +955,8 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
   if (!std::isfinite(scale)) return MIP_EINVAL;
   const int group = num_heads / num_kv_heads;
   const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
-  const KernelPair kp = pick_kernel(wl.algo == Algo::kStream ? Algo::kMfma : wl.algo, dtype, head_dim, group);
+  const int vsplit = wl.algo == Algo::kValu ? valu_split(group) : 1;
+  const KernelPair kp = pick_kernel(wl.algo == Algo::kStream ? Algo::kMfma : wl.algo, dtype, head_dim, group / vsplit);
   if (!kp.part) return MIP_EUNSUPPORTED;
   const int64_t es = dtype == MIP_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return MIP_EINVAL;
@@ -1021,8 +1037,10 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
     return st == 0 ? MIP_OK : st;
   }
   if (app.slots) return MIP_EUNSUPPORTED;  // callers fuse only into the stream kernel
-  hipLaunchKernelGGL(kp.part, dim3(wl.nparts, num_kv_heads, batch), dim3(kNW * kWave), 0, s, a);
-  if (wl.nparts > 1) hipLaunchKernelGGL(kp.merge, dim3(num_kv_heads, batch), dim3(256), 0, s, a);
+  if (static_cast<int64_t>(num_kv_heads) * vsplit > 65535) return MIP_EUNSUPPORTED;
+  a.gsplit = vsplit;
+  hipLaunchKernelGGL(kp.part, dim3(wl.nparts, num_kv_heads * vsplit, batch), dim3(kNW * kWave), 0, s, a);
+  if (wl.nparts > 1) hipLaunchKernelGGL(kp.merge, dim3(num_kv_heads * vsplit, batch), dim3(256), 0, s, a);
   return status_from_hip(hipGetLastError());
 }
 

@@ -23,6 +23,9 @@ struct DecodeArgs {
   int64_t bt_stride;
   const int32_t* lens;
   int hq, hkv, bs, log2_bs, max_blocks;
+  // VALU kernel: workgroups per kv head (0 or 1: one). With gsplit > 1 workgroup y of the grid
+  // reads kv head y / gsplit and serves its G query heads y * G .. y * G + G - 1.
+  int gsplit;
   int part_tokens;
   int nparts;
   float scale_log2;

@@ -566,7 +566,7 @@ extern "C" int mip_paged_prefill(void* out, int64_t out_stride_tok, int64_t out_
   const int group = num_heads / num_kv_heads;
   if (dtype == MIP_F32 || (head_dim != 64 && head_dim != 128) || group > 16) {
     // Shapes without an MFMA prefill kernel: the VALU decode kernel, one workgroup per
-    // (new token, kv head) over that token's keys (MIP_EUNSUPPORTED past 8 heads per kv head).
+    // (new token, kv head) over that token's keys (per group of at most 8 of its query heads).
     if (num_cache_blocks > INT32_MAX) return MIP_EINVAL;
     return decode::valu_prefill_launch(out, out_stride_tok, out_stride_head, q, q_stride_tok, q_stride_head, k_cache,
                                        v_cache, num_cache_blocks, block_tables, bt_stride, cu_q, ctx_start, num_seqs,

@@ -223,12 +223,10 @@ def algo(request):
 @pytest.mark.parametrize("dtype", list(DTYPES))
 @pytest.mark.parametrize("d,hq,hkv,bs", [(64, 14, 2, 16), (128, 28, 4, 32), (8, 4, 2, 4), (64, 8, 8, 16),
                                          (32, 6, 2, 8), (256, 8, 1, 16), (16, 5, 1, 2), (64, 14, 2, 4),
-                                         (128, 16, 1, 8), (64, 24, 2, 64)])
+                                         (128, 16, 1, 8), (64, 24, 2, 64), (32, 11, 1, 16)])
 def test_paged_decode_shapes(gpu, dtype, d, hq, hkv, bs, algo):
     announce(f"paged_decode {dtype} d={d} hq={hq} hkv={hkv} bs={bs} algo={algo}")
     lens = [1, bs - 1 if bs > 1 else 1, bs, bs + 1, 37, 511, 512, 513, 1200, 2049]
-    if hq // hkv > 8 and (dtype == "float32" or d not in (64, 128) or algo == "valu"):
-        pytest.skip("query groups above 8 exist only in the MFMA kernel (16-bit, head_dim 64/128)")
     _check_decode(gpu, dtype, len(lens), hq, hkv, d, bs, lens, seed=d + hq)
 
 
@@ -253,8 +251,6 @@ def test_fused_append_decode_equals_two_calls(gpu, dtype, d, hq, hkv, bs, algo):
     from engine import paged_ops
 
     announce(f"fused append+decode {dtype} d={d} hq={hq} hkv={hkv} bs={bs} algo={algo}")
-    if hq // hkv > 8 and (dtype == "float32" or algo == "valu"):
-        pytest.skip("query groups above 8 exist only in the MFMA kernels")
     lens = [1, bs, bs + 1, 37, 513, 1200, 2049, 5, 0, 64, 17]  # keys after the append (positions + 1)
     batch = len(lens)
     q, k_pool, v_pool, tables, bt, width = _random_case(dtype, batch, hq, hkv, d, bs, lens, nb_extra=4, seed=d + bs)

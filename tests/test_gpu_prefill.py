@@ -94,11 +94,14 @@ def test_paged_prefill_matches_f64(gpu, dtype, d, hq, hkv, bs, case):
 
 @pytest.mark.parametrize("dtype,d,hq,hkv,bs", [("float32", 64, 14, 2, 16), ("float32", 128, 8, 2, 32),
                                                ("float16", 32, 8, 2, 16), ("bfloat16", 256, 4, 2, 16),
-                                               ("float32", 8, 4, 4, 4), ("float16", 16, 5, 1, 2)])
+                                               ("float32", 8, 4, 4, 4), ("float16", 16, 5, 1, 2),
+                                               ("float32", 64, 16, 1, 16), ("float16", 32, 24, 2, 8),
+                                               ("bfloat16", 16, 11, 1, 16)])
 @pytest.mark.parametrize("case", range(len(CASES)))
 def test_paged_prefill_valu_shapes(gpu, dtype, d, hq, hkv, bs, case):
     """Shapes without an MFMA prefill kernel (fp32, head sizes other than 64/128) run the VALU
-    decode kernel, one workgroup per (new token, kv head); same bar against float64."""
+    decode kernel, one workgroup per (new token, kv head, group of at most 8 query heads: 16 =
+    2 x 8, 12 = 2 x 6, 11 = 11 x 1); same bar against float64."""
     from engine import paged_ops
 
     starts, lengths = CASES[case]
@@ -127,11 +130,11 @@ def test_paged_prefill_valu_stale_rows_and_loose_grid(gpu):
 
 
 def test_paged_prefill_unsupported_shape_raises(gpu):
-    """No kernel for fp32 with more than 8 query heads per kv head: the call raises (no fallback)."""
+    """No kernel for a head size that is not a power of two: the call raises (no fallback)."""
     from engine import _native, paged_ops
 
-    announce("paged_prefill fp32 group 16: unsupported")
-    dev, _ = build(gpu, "float32", 64, 16, 1, 16, [0], [4], seed=1)
+    announce("paged_prefill fp32 head_dim 96: unsupported")
+    dev, _ = build(gpu, "float32", 96, 16, 1, 16, [0], [4], seed=1)
     with pytest.raises(_native.NativeError, match="unsupported"):
         paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], 4)
 
