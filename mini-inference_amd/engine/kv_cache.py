@@ -566,8 +566,8 @@ class PackedPrefillContext:
                     sin: torch.Tensor) -> torch.Tensor:
         """``apply_rope`` (engine/model.py:249) + :meth:`attend`, with the rotation fused into the append.
 
-        ``cos``/``sin`` are ``[1, 1, N, D]``; q and k are rotated in place, so the SDPA below
-        sees the same tensors as after ``apply_rope``.
+        ``cos``/``sin`` are ``[1, 1, N, D]``; q and k are rotated in place, so the prefill
+        attention below sees the same tensors as after ``apply_rope``.
         """
         k_layer, v_layer = self.cache.k[layer_idx], self.cache.v[layer_idx]
         paged_ops.rope_kv_append(q[0].transpose(0, 1), k[0].transpose(0, 1), v[0].transpose(0, 1), cos[0, 0],
