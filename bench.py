@@ -26,7 +26,8 @@ Reported (one JSON line on stdout):
   prefill       packed prefill attention over a cached prefix (64 forks of a 520-token prefix,
                 suffixes U[32, 512], fp16): time per layer and TFLOP/s against the fp16 MFMA peak
   long_context  the same append + attention step at 28 query / 4 KV heads, head_dim 128, bf16,
-                B=128, contexts log-uniform in [512, 8192], block 32: time per layer and GB/s
+                B=128, contexts log-uniform in [512, 8192], block 32: time per layer and GB/s,
+                and the read probe over the same bytes as 8 KiB chunks (hbm_ceiling)
   cpu_baseline  the reference's torch CPU path (index_put_ append + table gather + SDPA,
                 the oracle's restatement) timed on this host's cores for one layer, fp32
 
@@ -722,6 +723,17 @@ def main() -> int:
             result["long_context"] = long_context_measure(dev)
             lc = result["long_context"]
             log(f"long-context decode: {lc['us_per_layer']} us/layer, {lc['achieved']} GB/s ({lc['frac']:.1%} of peak)")
+            if not args.no_probe:
+                # The same bytes through the read probe, as 8 KiB chunks (one block's K or V rows of
+                # one kv head at this shape); 4 disjoint sets of the 4 GiB buffer, cycled.
+                lh = hbm_ceiling(dev, lc["bytes_per_layer"], chunk=8192, sets=4, iters=12, grids=(2048, 4096, 8192))
+                lh["decode_call_frac_of_layer_window"] = round(lc["achieved"] / lh["random_chunks_layer_window"]["GBps"], 4)
+                lc["hbm_ceiling"] = lh
+                log(f"long-context hbm probe: {lh['bytes']} B as random 8 KiB chunks {lh['random_chunks']['us']} us "
+                    f"({lh['random_chunks']['GBps']} GB/s), within a layer-sized window "
+                    f"{lh['random_chunks_layer_window']['us']} us ({lh['random_chunks_layer_window']['GBps']} GB/s; the "
+                    f"call reaches {lh['decode_call_frac_of_layer_window']:.1%} of it), sequential "
+                    f"{lh['sequential']['us']} us ({lh['sequential']['GBps']} GB/s)")
         except Exception as exc:
             log(f"long-context decode measurement failed: {exc!r}")
             result["long_context"] = None
