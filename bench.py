@@ -560,7 +560,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one MI355X: the paged decode path runs on a single GPU here "
-              "(--gpus 1); multi-GPU runs are not part of this build.", file=sys.stderr)
+              "(--gpus 1); multi-GPU runs are not supported.", file=sys.stderr)
         return 2
 
     import torch

@@ -1,8 +1,8 @@
 """Oracle: CPU restatement of the reference's paged KV-cache path.
 
 TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the checker or as
-the timed CPU baseline. The product (``mini-inference_amd/engine``) never calls it.
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the reference results are checked
+against or as the timed CPU baseline. The product (``mini-inference_amd/engine``) never calls it.
 
 Each function restates one piece of the reference (Ham12-3/mini-inference) and cites it:
 

@@ -1,5 +1,5 @@
 """Seeded allocator traces shared by make_alloc_golden.py (which runs them on the reference's
-allocator in the build container) and tests/test_host.py (which runs them on this build's).
+allocator in the build container) and tests/test_host.py (which runs them on mini-inference_amd's).
 
 Test infrastructure. A trace only calls the allocator's public API, the way the reference
 scheduler drives it (engine/scheduler.py:89-125, engine/engine.py:289-298): admission with

@@ -5,18 +5,18 @@ allocator.
 
 Runs in the build container only: it imports ``engine.kv_cache.PagedKVCache`` from the
 reference checkout at /root/reference (pure Python over an OrderedDict; the pool tensors are
-made tiny: 1 layer, 1 kv head, head_dim 1, on the CPU). This build's allocator claims to hand
+made tiny: 1 layer, 1 kv head, head_dim 1, on the CPU). The engine package's allocator claims to hand
 out the same block ids as the reference's under any trace, and the reference's own tests pin
 that only on short traces (tests/test_kv_cache.py:163-175, :210-242), so this script records:
 
 * the 256 block tables of the bf16 B=256 workload (log-uniform contexts 128-4096, block 16,
-  32,768-block pool scrambled by 5,000 seeded alloc / grow / free events), driven by this
-  build's own workload code (``workloads.churn`` and ``workloads.context_lengths``, run
-  against the reference allocator exactly as ``build_decode_batch`` runs them against this
-  build's);
+  32,768-block pool scrambled by 5,000 seeded alloc / grow / free events), driven by the
+  engine package's own workload code (``workloads.churn`` and ``workloads.context_lengths``, run
+  against the reference allocator exactly as ``build_decode_batch`` runs them against
+  its own);
 * one digest per event of a 3,000-event prefix-caching trace (``alloc_trace.prefix_churn``).
 
-tests/test_host.py replays both on this build's allocator and compares. The fixture holds
+tests/test_host.py replays both on the engine package's allocator and compares. The fixture holds
 data only (block ids and digests).
 """
 
@@ -40,8 +40,8 @@ sys.path.insert(0, str(HERE))
 import alloc_trace  # noqa: E402
 
 
-def this_builds_workloads():
-    """This build's engine package under the name ``mi_engine`` (the reference's is ``engine``)."""
+def engine_workloads():
+    """mini-inference_amd's engine package under the name ``mi_engine`` (the reference's is ``engine``)."""
     pkg = ROOT / "mini-inference_amd" / "engine"
     spec = importlib.util.spec_from_file_location("mi_engine", pkg / "__init__.py",
                                                   submodule_search_locations=[str(pkg)])
@@ -75,7 +75,7 @@ def config3_tables(cache_cls, workloads) -> list[list[int]]:
 
 
 def main() -> None:
-    workloads = this_builds_workloads()
+    workloads = engine_workloads()
     ref_cls = reference_cache_class()
     tables = config3_tables(ref_cls, workloads)
     pool = alloc_trace.PREFIX_POOL

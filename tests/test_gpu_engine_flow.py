@@ -6,7 +6,7 @@ with ``allocate(num_tokens, token_ids)`` (a prefix-cache hit shares blocks), pre
 packed forward pass over their uncached tokens, registered with ``register_prefix``, then
 decoded one token per step; when ``ensure_capacity`` fails the newest request is preempted
 (``free``) and later recomputes its prompt plus what it had generated. This test restates that
-flow (test infrastructure, not part of the product) over this build's cache and kernels and a
+flow (test infrastructure, not part of the product) over mini-inference_amd's cache and kernels and a
 random-init Qwen2 model, and checks every logit row it produces against each request run alone
 with no prefix caching and no preemption, as tests/test_engine_parity.py:78-116 of the
 reference does with real weights. Tokens are teacher-forced (fixed in advance), so a rounding

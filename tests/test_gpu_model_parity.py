@@ -1,4 +1,4 @@
-"""The model through this build's contexts against the same model through the reference's own
+"""The model through mini-inference_amd's contexts against the same model through the reference's own
 formulation of attention, logits compared.
 
 A random-init Qwen2 (2 layers of the Qwen2.5-0.5B attention shape) prefills four prompts in
