@@ -399,10 +399,13 @@ def copy_floor(dev, nbytes: int, sets: int, iters: int = 40) -> float:
 
 def copy_measure(dev, iters: int = 40, sets: int = 8) -> dict:
     """Copy-on-write of the shared-prefix workload: each of 64 forks copies its partially
-    filled last shared block, every layer, K and V (``mip_copy_blocks``, one launch for all
-    pairs). Pools of 24 layers at the Qwen2.5-0.5B shape (fp16, 2 kv heads, d64, block 16);
-    ``sets`` disjoint sets of 64 (src, dst) pairs are cycled so no launch re-reads what the
-    last one touched. bytes = read + write of 24 * 2 * 2 KiB per pair.
+    filled last shared block, every layer, K and V, in one launch for all pairs. Timed as
+    PagedKVCache.copy_blocks issues it, with the pairs built on the host and passed in the
+    kernel arguments (``mip_copy_blocks_host``); ``device_pairs`` times the same copies with
+    the pairs read from device memory (``mip_copy_blocks``). Pools of 24 layers at the
+    Qwen2.5-0.5B shape (fp16, 2 kv heads, d64, block 16); ``sets`` disjoint sets of 64
+    (src, dst) pairs are cycled so no launch re-reads what the last one touched. bytes = read
+    + write of 24 * 2 * 2 KiB per pair.
     """
     import random
 
@@ -419,27 +422,33 @@ def copy_measure(dev, iters: int = 40, sets: int = 8) -> dict:
     v.normal_(0.0, 1.0, generator=gen)
     ids = list(range(nb))
     random.Random(5).shuffle(ids)
-    sets_t = [torch.tensor([[ids[2 * (i * pairs_per + j)], ids[2 * (i * pairs_per + j) + 1]] for j in range(pairs_per)],
-                           dtype=torch.int64, device=dev) for i in range(sets)]
-    calls = [paged_ops.prepare_copy_blocks(k, v, t) for t in sets_t]
-    it = [0]
+    host_sets = [[(ids[2 * (i * pairs_per + j)], ids[2 * (i * pairs_per + j) + 1]) for j in range(pairs_per)]
+                 for i in range(sets)]
 
-    def call():
-        calls[it[0] % sets]()
-        it[0] += 1
+    def timed(pair_sets) -> float:
+        calls = [paged_ops.prepare_copy_blocks(k, v, p) for p in pair_sets]
+        it = [0]
 
-    for _ in range(sets):
-        call()
-    torch.cuda.synchronize()
-    t = time_loop(call, iters)
+        def call():
+            calls[it[0] % sets]()
+            it[0] += 1
+
+        for _ in range(sets):
+            call()
+        torch.cuda.synchronize()
+        return time_loop(call, iters)
+
+    t = timed(host_sets)
+    t_dev = timed([torch.tensor(p, dtype=torch.int64, device=dev) for p in host_sets])
     nbytes = 2 * pairs_per * layers * 2 * hkv * bs * d * 2
     gbs = nbytes / t / 1e9
     floor = copy_floor(dev, nbytes, sets=sets)
     return {
         "workload": f"copy-on-write of {pairs_per} partially filled shared blocks (one per fork), {layers} layers, "
                     "K and V, fp16, 2 kv heads d64, block 16",
-        "kernel": "copy_blocks_kernel<16>",
+        "kernel": "copy_blocks_kernel<16, InlinePairs> (pairs in the kernel arguments)",
         "us": round(t * 1e6, 2),
+        "device_pairs_us": round(t_dev * 1e6, 2),
         "copy_floor_us": round(floor * 1e6, 2),
         "bound": "hbm",
         "achieved": round(gbs, 1),
@@ -712,8 +721,9 @@ def main() -> int:
         try:
             result["block_copy"] = copy_measure(dev)
             bc = result["block_copy"]
-            log(f"block copy: {bc['us']} us, {bc['achieved']} GB/s ({bc['frac']:.1%} of peak); "
-                f"a device copy of the same bytes takes {bc['copy_floor_us']} us")
+            log(f"block copy: {bc['us']} us, {bc['achieved']} GB/s ({bc['frac']:.1%} of peak; pairs read from "
+                f"device memory {bc['device_pairs_us']} us); a device copy of the same bytes takes "
+                f"{bc['copy_floor_us']} us")
         except Exception as exc:
             log(f"block copy measurement failed: {exc!r}")
             result["block_copy"] = None

@@ -318,6 +318,21 @@ int mip_copy_blocks(void* k_cache, void* v_cache, const int64_t* pairs, int32_t 
                     int32_t num_layers, int64_t num_cache_blocks, int64_t block_bytes,
                     void* stream);
 
+/*
+ * mip_copy_blocks with `pairs` in host memory: the same copy and the same rules. The pairs
+ * travel in the kernel arguments, MIP_COPY_INLINE_PAIRS per launch (one launch per group), so
+ * the copy needs no upload of the pairs and reads no pair list from device memory before its
+ * data. `pairs` may be reused or freed as soon as the call returns. Like any kernel argument,
+ * the pairs are fixed when a stream capture records the call.
+ *
+ * No reference counterpart (as mip_copy_blocks); PagedKVCache.copy_blocks uses it for the
+ * copy-on-write pairs it builds on the host.
+ */
+#define MIP_COPY_INLINE_PAIRS 128
+int mip_copy_blocks_host(void* k_cache, void* v_cache, const int64_t* pairs, int32_t n_pairs,
+                         int32_t num_layers, int64_t num_cache_blocks, int64_t block_bytes,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

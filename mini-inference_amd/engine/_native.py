@@ -31,6 +31,7 @@ EXPORTED = (
     "mip_paged_decode_plan_bytes",
     "mip_paged_prefill",
     "mip_copy_blocks",
+    "mip_copy_blocks_host",
 )
 
 # Measurement helpers in the same library (include/mipaged_probe.h), outside the drop-in ABI.
@@ -81,6 +82,7 @@ _SIGNATURES = {
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp],
     ),
     "mip_copy_blocks": (_c.c_int, [_vp, _vp, _vp, _i32, _i32, _i64, _i64, _vp]),
+    "mip_copy_blocks_host": (_c.c_int, [_vp, _vp, _vp, _i32, _i32, _i64, _i64, _vp]),
     "mip_hbm_read_probe": (_c.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _i32, _vp]),
 }
 

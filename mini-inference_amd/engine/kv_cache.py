@@ -236,14 +236,16 @@ class PagedKVCache:
         return pairs
 
     def copy_blocks(self, pairs: Sequence[tuple[int, int]] | torch.Tensor) -> None:
-        """``k[:, dst] = k[:, src]`` and ``v[:, dst] = v[:, src]`` for every (src, dst), all layers, on device."""
-        if isinstance(pairs, torch.Tensor):
-            t = pairs.to(device=self.k.device, dtype=torch.int64).reshape(-1, 2).contiguous()
-        else:
-            if len(pairs) == 0:
-                return
-            t = torch.from_numpy(np.asarray(pairs, dtype=np.int64).reshape(-1, 2)).to(self.k.device)
-        paged_ops.copy_blocks(self.k, self.v, t)
+        """``k[:, dst] = k[:, src]`` and ``v[:, dst] = v[:, src]`` for every (src, dst), all layers, on device.
+
+        Pairs built on the host (the copy-on-write pairs of :meth:`prepare_writes`) go to the
+        kernel in its arguments (``mip_copy_blocks_host``), with no upload; a tensor on the
+        pool's device is read there (``mip_copy_blocks``)."""
+        if isinstance(pairs, torch.Tensor) and pairs.is_cuda:
+            pairs = pairs.to(device=self.k.device, dtype=torch.int64).reshape(-1, 2).contiguous()
+        elif len(pairs) == 0:
+            return
+        paged_ops.copy_blocks(self.k, self.v, pairs)
 
     # ----------------------------------------------------------------- device-resident tables
     def _log_table(self, slot: int) -> None:

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from . import _native
@@ -503,28 +504,56 @@ def paged_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cac
     return out
 
 
-def prepare_copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs: torch.Tensor):
-    """Validate a :func:`copy_blocks` call once; returns a :class:`PreparedCall` (or a no-op for no pairs)."""
-    _require_device(k_pool, v_pool, pairs)
+def _copy_shape(k_pool: torch.Tensor, v_pool: torch.Tensor) -> tuple[int, int, int]:
     if k_pool.shape != v_pool.shape or k_pool.dim() != 5 or not (k_pool.is_contiguous() and v_pool.is_contiguous()):
         raise ValueError("k_pool/v_pool must be contiguous [L, num_blocks, Hkv, block_size, D] tensors of one shape")
-    if pairs.dtype != torch.int64 or pairs.dim() != 2 or pairs.shape[1] != 2 or not pairs.is_contiguous():
-        raise ValueError("pairs must be contiguous int64 [n, 2]")
-    n = pairs.shape[0]
+    return k_pool.shape[0], k_pool.shape[1], k_pool[0, 0].numel() * k_pool.element_size()
+
+
+def _host_pairs(pairs) -> np.ndarray:
+    """``pairs`` (a CPU tensor, an array or a sequence of (src, dst)) as contiguous int64 [n, 2]."""
+    if isinstance(pairs, torch.Tensor):
+        pairs = pairs.numpy()
+    arr = np.ascontiguousarray(np.asarray(pairs, dtype=np.int64).reshape(-1, 2))
+    return arr
+
+
+def prepare_copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs):
+    """Validate a :func:`copy_blocks` call once; returns a :class:`PreparedCall` (or a no-op for no pairs).
+
+    ``pairs`` on the pool's device: ``mip_copy_blocks`` reads them from device memory (a
+    graph replay sees later writes to that tensor). Anything else (a CPU tensor, an array, a
+    sequence of (src, dst)): ``mip_copy_blocks_host`` passes them in the kernel arguments, as
+    they are when the call is prepared.
+    """
+    _require_device(k_pool, v_pool)
+    num_layers, nb, block_bytes = _copy_shape(k_pool, v_pool)
+    stream = _stream_ptr(k_pool.device)
+    if isinstance(pairs, torch.Tensor) and pairs.is_cuda:
+        _require_device(pairs)
+        if pairs.dtype != torch.int64 or pairs.dim() != 2 or pairs.shape[1] != 2 or not pairs.is_contiguous():
+            raise ValueError("pairs must be contiguous int64 [n, 2]")
+        if pairs.device != k_pool.device:
+            raise ValueError("pairs on a device must be on the pool's device")
+        n = pairs.shape[0]
+        if n == 0:
+            return _noop
+        args = (k_pool.data_ptr(), v_pool.data_ptr(), pairs.data_ptr(), n, num_layers, nb, block_bytes, stream)
+        return PreparedCall(_native.load().mip_copy_blocks, args, "mip_copy_blocks", (k_pool, v_pool, pairs))
+    arr = _host_pairs(pairs)
+    n = arr.shape[0]
     if n == 0:
         return _noop
-    num_layers, nb = k_pool.shape[0], k_pool.shape[1]
-    block_bytes = k_pool[0, 0].numel() * k_pool.element_size()
-    args = (k_pool.data_ptr(), v_pool.data_ptr(), pairs.data_ptr(), n, num_layers, nb, block_bytes,
-            _stream_ptr(k_pool.device))
-    return PreparedCall(_native.load().mip_copy_blocks, args, "mip_copy_blocks", (k_pool, v_pool, pairs))
+    args = (k_pool.data_ptr(), v_pool.data_ptr(), arr.ctypes.data, n, num_layers, nb, block_bytes, stream)
+    return PreparedCall(_native.load().mip_copy_blocks_host, args, "mip_copy_blocks_host", (k_pool, v_pool, arr))
 
 
-def copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs: torch.Tensor) -> None:
+def copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs) -> None:
     """Copy whole blocks, every layer, K and V: ``pool[:, dst] = pool[:, src]`` per (src, dst) row.
 
     ``k_pool``/``v_pool``: ``[num_layers, num_blocks + 1, Hkv, block_size, D]`` contiguous.
-    ``pairs``: int64 ``[n, 2]`` on the pool's device. Bitwise copy (no reference
-    counterpart; used for copy-on-write of shared prefix blocks).
+    ``pairs``: int64 ``[n, 2]`` on the pool's device, or (src, dst) pairs on the host (a CPU
+    tensor, an array or a sequence), which travel in the kernel arguments with no upload.
+    Bitwise copy (no reference counterpart; used for copy-on-write of shared prefix blocks).
     """
     prepare_copy_blocks(k_pool, v_pool, pairs)()

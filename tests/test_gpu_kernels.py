@@ -136,14 +136,16 @@ def test_append_narrow_rows_and_skipped_slots(gpu, dtype, d):
 # ----------------------------------------------------------------------------- block copy
 
 
+@pytest.mark.parametrize("where", ["device", "host"])
 @pytest.mark.parametrize("dtype,hkv,bs,d", [("bfloat16", 2, 16, 64), ("float32", 2, 16, 64),
                                             ("bfloat16", 4, 32, 128), ("float32", 1, 1, 3)])
-def test_copy_blocks_bit_exact(gpu, dtype, hkv, bs, d):
+def test_copy_blocks_bit_exact(gpu, dtype, hkv, bs, d, where):
     """Whole-block copies, all layers, K and V; a 32 KiB block (4 kv heads x 32 x 128) takes
-    several chunk rounds per thread, a 12-byte block the 4-byte chunk width."""
+    several chunk rounds per thread, a 12-byte block the 4-byte chunk width. Pairs in device
+    memory (mip_copy_blocks) and on the host (mip_copy_blocks_host, in the kernel arguments)."""
     from engine import paged_ops
 
-    announce(f"copy_blocks {dtype} hkv={hkv} bs={bs} d={d}")
+    announce(f"copy_blocks {dtype} hkv={hkv} bs={bs} d={d} pairs on the {where}")
     dt = DTYPES[dtype]
     g = torch.Generator().manual_seed(6)
     layers, nb = 3, 40
@@ -154,10 +156,47 @@ def test_copy_blocks_bit_exact(gpu, dtype, hkv, bs, d):
     pairs = [(ids[i], ids[i + 12]) for i in range(12)] + [(3, -1), (nb + 5, 4)]  # last two are skipped
     kc, vc = storage(k), storage(v)
     ref.copy_blocks(kc, vc, pairs[:12])
-    paged_ops.copy_blocks(k, v, torch.tensor(pairs, dtype=torch.int64, device=gpu))
+    paged_ops.copy_blocks(k, v, torch.tensor(pairs, dtype=torch.int64, device=gpu) if where == "device" else pairs)
     torch.cuda.synchronize()
     assert np.array_equal(storage(k), kc)
     assert np.array_equal(storage(v), vc)
+
+
+def test_copy_blocks_host_pairs_over_several_launches(gpu):
+    """300 host pairs (three launches of at most 128 pairs in the kernel arguments), ids past
+    the int32 range and negative ones skipped, against the oracle; then the same copy through
+    PagedKVCache.copy_blocks with a list and with a CPU tensor."""
+    from engine import paged_ops
+    from engine.kv_cache import PagedKVCache
+
+    announce("copy_blocks_host: 300 pairs, 3 launches")
+    g = torch.Generator().manual_seed(8)
+    layers, nb, hkv, bs, d = 2, 700, 2, 16, 64
+    k = torch.randn(layers, nb + 1, hkv, bs, d, generator=g).to(torch.bfloat16).to(gpu)
+    v = torch.randn(layers, nb + 1, hkv, bs, d, generator=g).to(torch.bfloat16).to(gpu)
+    ids = random.Random(9).sample(range(nb + 1), 600)
+    pairs = [(ids[i], ids[i + 300]) for i in range(300)]
+    pairs[5] = (pairs[5][0], 1 << 40)   # skipped: past the pool (and past int32)
+    pairs[200] = (-3, pairs[200][1])    # skipped
+    kc, vc = storage(k), storage(v)
+    ref.copy_blocks(kc, vc, [p for i, p in enumerate(pairs) if i not in (5, 200)])
+    paged_ops.copy_blocks(k, v, np.asarray(pairs, dtype=np.int64))
+    torch.cuda.synchronize()
+    assert np.array_equal(storage(k), kc)
+    assert np.array_equal(storage(v), vc)
+
+    cache = PagedKVCache(num_layers=layers, num_kv_heads=hkv, head_dim=d, num_blocks=nb, block_size=bs, max_seqs=4,
+                         max_len=64, dtype=torch.bfloat16, device=gpu)
+    cache.k.copy_(k)
+    cache.v.copy_(v)
+    more = [(ids[i], ids[i + 1]) for i in range(0, 20, 2)]
+    kc2, vc2 = storage(cache.k), storage(cache.v)
+    ref.copy_blocks(kc2, vc2, more)
+    cache.copy_blocks(more[:5])
+    cache.copy_blocks(torch.tensor(more[5:], dtype=torch.int64))
+    torch.cuda.synchronize()
+    assert np.array_equal(storage(cache.k), kc2)
+    assert np.array_equal(storage(cache.v), vc2)
 
 
 # ----------------------------------------------------------------------------- paged decode attention

@@ -381,10 +381,11 @@ def test_abi_host_checks_return_before_launch(lib):
     assert pf(*st) == E                                 # table stride below max_blocks
     nul = list(pargs); nul[13] = 2
     assert pf(*nul) == E                                # null pointers
-    cp = lib.mip_copy_blocks
-    assert cp(None, None, None, 0, 24, 100, 8192, None) == OK
-    assert cp(None, None, None, 3, 0, 100, 8192, None) == E
-    assert cp(None, None, None, 3, 24, 100, 8192, None) == E
+    for cp in (lib.mip_copy_blocks, lib.mip_copy_blocks_host):
+        assert cp(None, None, None, 0, 24, 100, 8192, None) == OK  # no pairs
+        assert cp(None, None, None, 3, 0, 100, 8192, None) == E    # no layers
+        assert cp(None, None, None, -1, 24, 100, 8192, None) == E  # negative count
+        assert cp(None, None, None, 3, 24, 100, 8192, None) == E   # pairs but null pointers
 
 
 def test_decode_algo_setting(lib):
