@@ -1158,6 +1158,10 @@ __global__ __launch_bounds__(256) void paged_decode_stream_fold(StreamArgs sa) {
 // grid-stride loops, the wavefront ranges, the segment records for the merge kernel and one
 // descriptor per tile. Layout: kPlanHeader / kPlanWave / kPlanSeg / tile descriptors.
 constexpr int kPlanThreads = 256;
+#ifndef MIP_PLAN_TILES_PER_THREAD
+#define MIP_PLAN_TILES_PER_THREAD 2
+#endif
+constexpr int kPlanTilesPerThread = MIP_PLAN_TILES_PER_THREAD;
 
 struct PlanArgs {
   const int32_t* lens;
@@ -1498,9 +1502,10 @@ int stream_plan_launch(const StreamConfig& cfg, const int32_t* lens, const int32
   p.seg_off = static_cast<int>(l.seg_off);
   p.tile_off = static_cast<int>(l.tile_off);
   p.wave_cap = static_cast<int>(l.wave_cap);
-  // Enough workgroups for about eight descriptors per thread at the largest tile count.
+  // Enough workgroups for about kPlanTilesPerThread descriptors per thread at the largest
+  // tile count.
   const int64_t max_tiles = (l.words - l.tile_off) / 2;
-  int64_t grid = (max_tiles + 8 * kPlanThreads - 1) / (8 * kPlanThreads);
+  int64_t grid = (max_tiles + kPlanTilesPerThread * kPlanThreads - 1) / (kPlanTilesPerThread * kPlanThreads);
   grid = grid < 1 ? 1 : (grid > 1024 ? 1024 : grid);
   const size_t lds = static_cast<size_t>(2 * batch + 1 + kPlanThreads / kWave) * 4;
   hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(static_cast<unsigned>(grid)), dim3(kPlanThreads), lds, stream, p);
