@@ -511,11 +511,11 @@ def _copy_shape(k_pool: torch.Tensor, v_pool: torch.Tensor) -> tuple[int, int, i
 
 
 def _host_pairs(pairs) -> np.ndarray:
-    """``pairs`` (a CPU tensor, an array or a sequence of (src, dst)) as contiguous int64 [n, 2]."""
+    """A private contiguous int64 [n, 2] copy of ``pairs`` (a CPU tensor, an array or a
+    sequence of (src, dst)), so a prepared call keeps the pairs it was prepared with."""
     if isinstance(pairs, torch.Tensor):
         pairs = pairs.numpy()
-    arr = np.ascontiguousarray(np.asarray(pairs, dtype=np.int64).reshape(-1, 2))
-    return arr
+    return np.array(pairs, dtype=np.int64, copy=True, order="C").reshape(-1, 2)
 
 
 def prepare_copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs):

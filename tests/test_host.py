@@ -419,6 +419,19 @@ def test_kernels_refuse_cpu_tensors():
                                  torch.zeros(1, 8), k, v, torch.zeros(1, dtype=torch.int64))
 
 
+def test_host_copy_pairs_are_a_private_copy():
+    """Pairs for mip_copy_blocks_host: any host form becomes a contiguous int64 [n, 2] copy, so
+    a prepared call keeps the pairs it was prepared with."""
+    a = np.array([[1, 2], [3, 4]], dtype=np.int64)
+    b = paged_ops._host_pairs(a)
+    a[0, 0] = 9
+    assert b.tolist() == [[1, 2], [3, 4]] and b.flags["C_CONTIGUOUS"] and b.dtype == np.int64
+    assert paged_ops._host_pairs([(5, 6)]).tolist() == [[5, 6]]
+    assert paged_ops._host_pairs(torch.tensor([[7, 8]], dtype=torch.int32)).dtype == np.int64
+    assert paged_ops._host_pairs(torch.arange(8).view(2, 4)[:, ::2]).tolist() == [[0, 2], [4, 6]]
+    assert paged_ops._host_pairs([]).shape == (0, 2)
+
+
 def test_missing_library_raises(tmp_path):
     with pytest.raises(_native.NativeLibraryMissing):
         _native.load(tmp_path / "absent.so")
