@@ -8,7 +8,8 @@
  *                           through per-sequence block tables (optionally fused with the
  *                           append, and driven by a per-step work plan).
  *   3. Block copy         : copy whole blocks (all layers, K and V) for copy-on-write of
- *                           shared prefix blocks.
+ *                           shared prefix blocks (the (src, dst) pairs in device memory, or
+ *                           in host memory, passed in the kernel arguments).
  *   4. Paged prefill attn : packed new tokens of several sequences over their cached
  *                           prefixes and themselves, causal, reading K/V pages in place.
  *
@@ -22,9 +23,10 @@
  * A slot is the flat token index  slot = block * block_size + offset.
  *
  * Conventions shared by every entry point
- *   - All pointers are device pointers owned by the caller; nothing here allocates,
- *     frees or synchronises. Work is enqueued on `stream` (a hipStream_t; NULL = the
- *     null stream) and the call returns immediately.
+ *   - All pointers are device pointers owned by the caller, except the pairs of
+ *     mip_copy_blocks_host, which the call reads on the host before it returns. Nothing
+ *     here allocates, frees or synchronises. Work is enqueued on `stream` (a hipStream_t;
+ *     NULL = the null stream) and the call returns immediately.
  *   - Strides are in ELEMENTS, not bytes. The last (head_dim) dimension must be
  *     contiguous.
  *   - Return value: MIP_OK (0) on success, MIP_EINVAL (-22) for arguments that fail the
