@@ -210,7 +210,8 @@ class PagedKVCache:
 
         For each sequence, every block touched by tokens ``[start, start + count)`` whose
         reference count is above one is replaced in that sequence's table by a fresh block,
-        and one :meth:`copy_blocks` launch copies all of them (all layers, K and V).
+        and one :meth:`copy_blocks` call copies all of them (all layers, K and V; one launch
+        per 128 pairs).
         Returns the ``(src, dst)`` pairs copied. Raises if the pool cannot supply them.
         """
         pairs: list[tuple[int, int]] = []
