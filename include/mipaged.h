@@ -314,7 +314,9 @@ size_t mip_paged_decode_workspace(int32_t batch, int32_t num_heads, int32_t num_
  * over a pool laid out [num_layers][num_cache_blocks][block_bytes].
  * `pairs` is int64 [n_pairs][2] = (src, dst). Pairs with an index outside
  * [0, num_cache_blocks) are skipped. Destinations must be distinct and must not be
- * the source of another pair in the same call.
+ * the source of another pair in the same call. One launch copies up to 2^24 - 1
+ * (pair, layer, K|V) units; a larger call is split into several launches in pair order.
+ * num_layers must be below 2^23 (MIP_EINVAL otherwise).
  */
 int mip_copy_blocks(void* k_cache, void* v_cache, const int64_t* pairs, int32_t n_pairs,
                     int32_t num_layers, int64_t num_cache_blocks, int64_t block_bytes,

@@ -95,10 +95,17 @@ int copy_setup(void* k_cache, void* v_cache, int32_t num_layers, int64_t num_cac
   return chunk;
 }
 
+// A launch's grid holds fewer than 2^32 work-items (HIP's limit on gridDim.x * blockDim.x),
+// so one launch copies at most this many (pair, layer, K|V) units.
+constexpr int64_t kMaxUnitsPerLaunch = ((int64_t{1} << 32) - 1) / kCopyThreads;
+
+// Pairs one launch may take at this layer count (0: not even one pair fits).
+int64_t pairs_per_launch(int32_t num_layers) { return kMaxUnitsPerLaunch / (2 * static_cast<int64_t>(num_layers)); }
+
 template <class P>
 int copy_launch(const CopyArgs& a, const P& ip, int64_t n_pairs, int chunk, hipStream_t s) {
   const int64_t units = n_pairs * a.num_layers * 2;
-  if (units >= (int64_t{1} << 31)) return MIP_EINVAL;
+  if (units > kMaxUnitsPerLaunch) return MIP_EINVAL;
   const dim3 grid(static_cast<unsigned>(units)), block(kCopyThreads);
   switch (chunk) {
     case 16: hipLaunchKernelGGL((copy_blocks_kernel<16, P>), grid, block, 0, s, a, ip); break;
@@ -120,10 +127,18 @@ extern "C" int mip_copy_blocks(void* k_cache, void* v_cache, const int64_t* pair
   if (n_pairs < 0 || num_layers <= 0 || num_cache_blocks <= 0 || block_bytes <= 0) return MIP_EINVAL;
   if (n_pairs == 0) return MIP_OK;
   if (!k_cache || !v_cache || !pairs) return MIP_EINVAL;
+  const int64_t per_launch = pairs_per_launch(num_layers);
+  if (per_launch < 1) return MIP_EINVAL;
   CopyArgs a;
   const int chunk = copy_setup(k_cache, v_cache, num_layers, num_cache_blocks, block_bytes, a);
-  a.pairs = pairs;
-  return copy_launch(a, NoPairs{}, n_pairs, chunk, static_cast<hipStream_t>(stream));
+  // One launch per per_launch pairs (a single one unless n_pairs * num_layers reaches 2^23).
+  for (int64_t p0 = 0; p0 < n_pairs; p0 += per_launch) {
+    const int64_t n = n_pairs - p0 < per_launch ? n_pairs - p0 : per_launch;
+    a.pairs = pairs + 2 * p0;
+    const int st = copy_launch(a, NoPairs{}, n, chunk, static_cast<hipStream_t>(stream));
+    if (st) return st;
+  }
+  return MIP_OK;
 }
 
 extern "C" int mip_copy_blocks_host(void* k_cache, void* v_cache, const int64_t* pairs, int32_t n_pairs,
@@ -132,13 +147,17 @@ extern "C" int mip_copy_blocks_host(void* k_cache, void* v_cache, const int64_t*
   if (n_pairs < 0 || num_layers <= 0 || num_cache_blocks <= 0 || block_bytes <= 0) return MIP_EINVAL;
   if (n_pairs == 0) return MIP_OK;
   if (!k_cache || !v_cache || !pairs) return MIP_EINVAL;
+  const int64_t fit = pairs_per_launch(num_layers);
+  if (fit < 1) return MIP_EINVAL;
+  const int32_t per_launch = fit < kInlinePairs ? static_cast<int32_t>(fit) : kInlinePairs;
   CopyArgs a;
   const int chunk = copy_setup(k_cache, v_cache, num_layers, num_cache_blocks, block_bytes, a);
-  // One launch per kInlinePairs pairs, their ids copied into the kernel arguments (an id
-  // outside [0, num_cache_blocks) becomes -1, which the kernel skips like the device variant).
+  // One launch per kInlinePairs pairs (fewer if the layer count is large), their ids copied into
+  // the kernel arguments (an id outside [0, num_cache_blocks) becomes -1, which the kernel skips
+  // like the device variant).
   InlinePairs ip;
-  for (int32_t p0 = 0; p0 < n_pairs; p0 += kInlinePairs) {
-    const int32_t n = n_pairs - p0 < kInlinePairs ? n_pairs - p0 : kInlinePairs;
+  for (int32_t p0 = 0; p0 < n_pairs; p0 += per_launch) {
+    const int32_t n = n_pairs - p0 < per_launch ? n_pairs - p0 : per_launch;
     for (int32_t i = 0; i < 2 * n; ++i) {
       const int64_t id = pairs[2 * static_cast<int64_t>(p0) + i];
       ip.id[i] = id >= 0 && id < num_cache_blocks && id <= INT32_MAX ? static_cast<int32_t>(id) : -1;

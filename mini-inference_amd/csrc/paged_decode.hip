@@ -152,12 +152,15 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_part(DecodeArgs a) {
   __shared__ float sh_l[kNW][G];
   __shared__ float sh_acc[kNW][G][D];
 
-  // Query heads h0 .. h0 + G - 1 of kv head kvh (a group of more than 8 heads is split over
-  // a.gsplit workgroups, each holding G of them in registers).
-  const int kvh = a.gsplit > 1 ? static_cast<int>(blockIdx.y) / a.gsplit : static_cast<int>(blockIdx.y);
+  // Query heads h0 .. h0 + nh - 1 of kv head kvh (a group of more than 8 heads is split over
+  // a.gsplit workgroups, each holding G of them in registers; the last one of a group holds
+  // nh <= G live heads, and its other register slots shadow head h0, whose results it drops).
+  const int y = static_cast<int>(blockIdx.y);
+  const int kvh = a.gsplit > 1 ? y / a.gsplit : y;
+  const int h0 = a.gsplit > 1 ? kvh * a.group + (y - kvh * a.gsplit) * G : y * G;
+  const int nh = a.gsplit > 1 ? min(G, a.group - (y - kvh * a.gsplit) * G) : G;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int h0 = static_cast<int>(blockIdx.y) * G;
 
   // Decode: (partition, kv head, sequence). Packed prefill: (sequence x new token, kv head),
   // one partition; the row's keys are its sequence's keys up to its own position.
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_part(DecodeArgs a) {
 
   S* out_base = reinterpret_cast<S*>(a.out);
   if (ctx <= 0) {
-    for (int i = tid; i < G * D; i += kNW * kWave) {
+    for (int i = tid; i < nh * D; i += kNW * kWave) {
       const int g = i / D, d = i % D;
       out_base[b * a.out_sb + (h0 + g) * a.out_sh + d] = from_f32<DT>(0.0f);
     }
@@ -199,7 +202,8 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_part(DecodeArgs a) {
     const char* qb = a.q + (static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(c) * CH) * ES;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const uint32_t* qp = reinterpret_cast<const uint32_t*>(qb + static_cast<int64_t>(h0 + g) * a.q_sh * ES);
+      const int hg = h0 + (g < nh ? g : 0);
+      const uint32_t* qp = reinterpret_cast<const uint32_t*>(qb + static_cast<int64_t>(hg) * a.q_sh * ES);
 #pragma unroll
       for (int i = 0; i < QW; ++i) qreg[g][i] = qp[i];
     }
@@ -348,7 +352,7 @@ __global__ __launch_bounds__(kNW * kWave) void paged_decode_part(DecodeArgs a) {
   __syncthreads();
 
   // ---- merge the kNW wavefronts; finish the sequence or hand the partition to the merge kernel.
-  for (int i = tid; i < G * D; i += kNW * kWave) {
+  for (int i = tid; i < nh * D; i += kNW * kWave) {
     const int g = i / D, d = i % D;
     float mx = -INFINITY;
 #pragma unroll
@@ -643,8 +647,11 @@ __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
   const int np_b = ctx > 0 ? (ctx + a.part_tokens - 1) / a.part_tokens : 1;
   if (np_b <= 1) return;
   S* out_base = reinterpret_cast<S*>(a.out);
-  const int h0 = hg * G;
-  for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
+  // The heads of workgroup y of the partition kernel (see paged_decode_part).
+  const int kvh = a.gsplit > 1 ? hg / a.gsplit : hg;
+  const int h0 = a.gsplit > 1 ? kvh * a.group + (hg - kvh * a.gsplit) * G : hg * G;
+  const int nh = a.gsplit > 1 ? min(G, a.group - (hg - kvh * a.gsplit) * G) : G;
+  for (int i = threadIdx.x; i < nh * D; i += blockDim.x) {
     const int g = i / D, d = i % D;
     const int64_t slot0 = (static_cast<int64_t>(b) * a.hq + h0 + g) * a.nparts;
     float mx = -INFINITY;
@@ -754,14 +761,15 @@ WsLayout ws_layout(int batch, int hq, int hkv, int d, int bs, int max_blocks, in
   return w;
 }
 
-// Workgroups per kv head of the VALU kernel: the smallest divisor of the query group that
-// leaves at most 8 query heads per workgroup (a workgroup keeps q, the running maxima and sums
-// and the accumulators of all its heads in registers). Each of them reads the kv head's keys
-// and values, so the K/V traffic grows by this factor.
-int valu_split(int g) {
-  for (int s = (g + 7) / 8; s < g; ++s)
-    if (g % s == 0) return s;
-  return g > 1 ? g : 1;
+// Workgroups per kv head of the VALU kernel: ceil(g / 8), so each holds at most 8 query heads
+// (a workgroup keeps q, the running maxima and sums and the accumulators of all its heads in
+// registers). Each of them reads the kv head's keys and values, so the K/V traffic grows by
+// this factor. valu_heads is the register slots per workgroup, ceil(g / split); the last
+// workgroup of a group masks the slots past the group's end.
+int valu_split(int g) { return g > 8 ? (g + 7) / 8 : 1; }
+int valu_heads(int g) {
+  const int s = valu_split(g);
+  return (g + s - 1) / s;
 }
 
 using KernelFn = void (*)(DecodeArgs);
@@ -868,7 +876,7 @@ int valu_prefill_launch(void* out, int64_t out_stride_tok, int64_t out_stride_he
                         float scale, int32_t dtype, hipStream_t stream) {
   const int group = num_heads / num_kv_heads;
   const int vsplit = valu_split(group);
-  const KernelPair kp = pick_kernel(Algo::kValu, dtype, head_dim, group / vsplit);
+  const KernelPair kp = pick_kernel(Algo::kValu, dtype, head_dim, valu_heads(group));
   if (!kp.part) return MIP_EUNSUPPORTED;
   const int64_t es = dtype == MIP_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return MIP_EINVAL;
@@ -909,6 +917,7 @@ int valu_prefill_launch(void* out, int64_t out_stride_tok, int64_t out_stride_he
   a.ctx_start = ctx_start;
   a.max_q_len = max_q_len;
   a.gsplit = vsplit;
+  a.group = group;
   hipLaunchKernelGGL(kp.part, dim3(static_cast<unsigned>(grid_x), num_kv_heads * vsplit, 1), dim3(kNW * kWave), 0,
                      stream, a);
   return status_from_hip(hipGetLastError());
@@ -956,7 +965,8 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
   const int group = num_heads / num_kv_heads;
   const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, dtype);
   const int vsplit = wl.algo == Algo::kValu ? valu_split(group) : 1;
-  const KernelPair kp = pick_kernel(wl.algo == Algo::kStream ? Algo::kMfma : wl.algo, dtype, head_dim, group / vsplit);
+  const KernelPair kp = pick_kernel(wl.algo == Algo::kStream ? Algo::kMfma : wl.algo, dtype, head_dim,
+                                    wl.algo == Algo::kValu ? valu_heads(group) : group);
   if (!kp.part) return MIP_EUNSUPPORTED;
   const int64_t es = dtype == MIP_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return MIP_EINVAL;
@@ -1039,6 +1049,7 @@ int paged_decode_impl(void* out, int64_t out_stride_b, int64_t out_stride_h, con
   if (app.slots) return MIP_EUNSUPPORTED;  // callers fuse only into the stream kernel
   if (static_cast<int64_t>(num_kv_heads) * vsplit > 65535) return MIP_EUNSUPPORTED;
   a.gsplit = vsplit;
+  a.group = group;
   hipLaunchKernelGGL(kp.part, dim3(wl.nparts, num_kv_heads * vsplit, batch), dim3(kNW * kWave), 0, s, a);
   if (wl.nparts > 1) hipLaunchKernelGGL(kp.merge, dim3(num_kv_heads * vsplit, batch), dim3(256), 0, s, a);
   return status_from_hip(hipGetLastError());

@@ -24,8 +24,11 @@ struct DecodeArgs {
   const int32_t* lens;
   int hq, hkv, bs, log2_bs, max_blocks;
   // VALU kernel: workgroups per kv head (0 or 1: one). With gsplit > 1 workgroup y of the grid
-  // reads kv head y / gsplit and serves its G query heads y * G .. y * G + G - 1.
+  // reads kv head y / gsplit and serves query heads kvh * group + (y % gsplit) * G .. + G - 1
+  // of its group of `group` heads; the last workgroup of a group masks the heads past its end
+  // (G = ceil(group / gsplit), so the split need not divide the group).
   int gsplit;
+  int group;
   int part_tokens;
   int nparts;
   float scale_log2;

@@ -96,6 +96,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ void dma16(const char* g, lchar_t* l) {
   __builtin_amdgcn_global_load_lds((gvoid_t*)g, (lvoid_t*)l, 16, 0, 0);
 }
+// K/V tile rows are read once per call: direct loads with the nontemporal cache policy (the
+// instruction's nt bit, cache-policy operand 2), which streams a 160 MB read of randomly placed
+// 2 KiB tiles about 10 % faster on gfx950 than the default policy.
+#ifndef MIP_KV_CPOL
+#define MIP_KV_CPOL 2
+#endif
+__device__ __forceinline__ void dma16_kv(const char* g, lchar_t* l) {
+  __builtin_amdgcn_global_load_lds((gvoid_t*)g, (lvoid_t*)l, 16, 0, MIP_KV_CPOL);
+}
 
 template <int OFF>
 __device__ __forceinline__ u32x4_t lds_b128(uint32_t addr) {
@@ -297,8 +306,8 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
         const int64_t row = row0 + (r < nvalid ? r : 0);
         const int lc = dma_pc ^ (r & (CPR - 1));
         const bool fresh = r == nr;
-        dma16(fresh ? nk + lc * 16 : a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
-        dma16(fresh ? nv + dma_pc * 16 : a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
+        dma16_kv(fresh ? nk + lc * 16 : a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
+        dma16_kv(fresh ? nv + dma_pc * 16 : a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
       }
     } else {
       // Small blocks: every row looks its block up; rows that are not keys re-read the
@@ -325,8 +334,8 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
         const int64_t row = ok ? static_cast<int64_t>(bl * a.hkv + pkvh) * a.bs + (tok & (a.bs - 1)) : row_first;
         const int lc = dma_pc ^ (r & (CPR - 1));
         const bool fresh = ok && tok == pL - 1 && static_cast<int64_t>(bl) * a.bs + (tok & (a.bs - 1)) == new_slot;
-        dma16(fresh ? nk + lc * 16 : a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
-        dma16(fresh ? nv + dma_pc * 16 : a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
+        dma16_kv(fresh ? nk + lc * 16 : a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
+        dma16_kv(fresh ? nv + dma_pc * 16 : a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
       }
     }
 #pragma unroll
@@ -640,8 +649,8 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
         const bool fresh = r == nr;
         const uint32_t ko = r < nvalid ? k_lane[j] : k_lane[j] - static_cast<uint32_t>(r * RB);
         const uint32_t vo = r < nvalid ? v_lane[j] : v_lane[j] - static_cast<uint32_t>(r * RB);
-        dma16(fresh ? nk + (k_lane[j] - r * RB) : kb + ko, st + R::K_OFF + j * 1024);
-        dma16(fresh ? nv + dma_pc * 16 : vb + vo, st + R::V_OFF + j * 1024);
+        dma16_kv(fresh ? nk + (k_lane[j] - r * RB) : kb + ko, st + R::K_OFF + j * 1024);
+        dma16_kv(fresh ? nv + dma_pc * 16 : vb + vo, st + R::V_OFF + j * 1024);
       }
     } else {
 #pragma unroll
@@ -649,8 +658,8 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
         const int r = r_lane[j];
         const uint32_t ko = r < nvalid ? k_lane[j] : k_lane[j] - static_cast<uint32_t>(r * RB);
         const uint32_t vo = r < nvalid ? v_lane[j] : v_lane[j] - static_cast<uint32_t>(r * RB);
-        dma16(kb + ko, st + R::K_OFF + j * 1024);
-        dma16(vb + vo, st + R::V_OFF + j * 1024);
+        dma16_kv(kb + ko, st + R::K_OFF + j * 1024);
+        dma16_kv(vb + vo, st + R::V_OFF + j * 1024);
       }
     }
     if (((meta >> 29) & 1u) || x == lo) {

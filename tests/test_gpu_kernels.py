@@ -199,6 +199,31 @@ def test_copy_blocks_host_pairs_over_several_launches(gpu):
     assert np.array_equal(storage(cache.v), vc2)
 
 
+def test_copy_blocks_device_pairs_over_several_launches(gpu):
+    """A device-pairs call with more (pair, layer, K|V) units than one launch's grid may hold
+    (2^24 - 1 workgroups of 256 threads): 2^22 + 1 pairs at 2 layers is split into two launches,
+    and every destination block equals its source afterwards."""
+    from engine import paged_ops
+
+    announce("copy_blocks device pairs: 2^22 + 1 pairs x 2 layers, two launches")
+    n = (1 << 22) + 1
+    layers, nb = 2, 2 * n
+    g = torch.Generator(device=gpu).manual_seed(10)
+    k = torch.randn(layers, nb + 1, 1, 1, 4, generator=g, device=gpu)  # 16-byte blocks
+    v = torch.randn(layers, nb + 1, 1, 1, 4, generator=g, device=gpu)
+    src = torch.arange(n, dtype=torch.int64, device=gpu)
+    pairs = torch.stack([src, src + n], dim=1).contiguous()
+    k_src, v_src = k[:, :n].clone(), v[:, :n].clone()
+    k_tail, v_tail = k[:, 2 * n:].clone(), v[:, 2 * n:].clone()
+    paged_ops.copy_blocks(k, v, pairs)
+    torch.cuda.synchronize()
+    assert torch.equal(k[:, n:2 * n], k_src) and torch.equal(v[:, n:2 * n], v_src)
+    assert torch.equal(k[:, :n], k_src) and torch.equal(v[:, :n], v_src)
+    assert torch.equal(k[:, 2 * n:], k_tail) and torch.equal(v[:, 2 * n:], v_tail)
+    del k, v, pairs, k_src, v_src
+    torch.cuda.empty_cache()
+
+
 # ----------------------------------------------------------------------------- paged decode attention
 
 
@@ -262,7 +287,8 @@ def algo(request):
 @pytest.mark.parametrize("dtype", list(DTYPES))
 @pytest.mark.parametrize("d,hq,hkv,bs", [(64, 14, 2, 16), (128, 28, 4, 32), (8, 4, 2, 4), (64, 8, 8, 16),
                                          (32, 6, 2, 8), (256, 8, 1, 16), (16, 5, 1, 2), (64, 14, 2, 4),
-                                         (128, 16, 1, 8), (64, 24, 2, 64), (32, 11, 1, 16)])
+                                         (128, 16, 1, 8), (64, 24, 2, 64), (32, 11, 1, 16), (64, 13, 1, 16),
+                                         (64, 27, 3, 16)])
 def test_paged_decode_shapes(gpu, dtype, d, hq, hkv, bs, algo):
     announce(f"paged_decode {dtype} d={d} hq={hq} hkv={hkv} bs={bs} algo={algo}")
     lens = [1, bs - 1 if bs > 1 else 1, bs, bs + 1, 37, 511, 512, 513, 1200, 2049]

@@ -96,12 +96,13 @@ def test_paged_prefill_matches_f64(gpu, dtype, d, hq, hkv, bs, case):
                                                ("float16", 32, 8, 2, 16), ("bfloat16", 256, 4, 2, 16),
                                                ("float32", 8, 4, 4, 4), ("float16", 16, 5, 1, 2),
                                                ("float32", 64, 16, 1, 16), ("float16", 32, 24, 2, 8),
-                                               ("bfloat16", 16, 11, 1, 16)])
+                                               ("bfloat16", 16, 11, 1, 16), ("float32", 64, 27, 3, 16)])
 @pytest.mark.parametrize("case", range(len(CASES)))
 def test_paged_prefill_valu_shapes(gpu, dtype, d, hq, hkv, bs, case):
     """Shapes without an MFMA prefill kernel (fp32, head sizes other than 64/128) run the VALU
     decode kernel, one workgroup per (new token, kv head, group of at most 8 query heads: 16 =
-    2 x 8, 12 = 2 x 6, 11 = 11 x 1); same bar against float64."""
+    2 x 8, 12 = 2 x 6, 11 = 6 + 5, 9 = 5 + 4 with the last workgroup masking a head slot);
+    same bar against float64."""
     from engine import paged_ops
 
     starts, lengths = CASES[case]

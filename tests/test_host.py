@@ -386,6 +386,7 @@ def test_abi_host_checks_return_before_launch(lib):
         assert cp(None, None, None, 3, 0, 100, 8192, None) == E    # no layers
         assert cp(None, None, None, -1, 24, 100, 8192, None) == E  # negative count
         assert cp(None, None, None, 3, 24, 100, 8192, None) == E   # pairs but null pointers
+        assert cp(16, 16, 16, 3, 1 << 23, 100, 16, None) == E      # one pair alone exceeds a launch's grid
 
 
 def test_decode_algo_setting(lib):
