@@ -474,6 +474,54 @@ def test_paged_decode_merge_streams(gpu, batch):
     assert torch.equal(out0, out1)
 
 
+@pytest.mark.parametrize("dtype,d,hq,hkv,bs,batch", [("bfloat16", 64, 14, 2, 16, 96), ("float16", 128, 28, 4, 32, 40),
+                                                     ("bfloat16", 128, 16, 1, 16, 80), ("float16", 64, 8, 8, 64, 12),
+                                                     ("bfloat16", 64, 14, 2, 16, 300)])
+def test_decode_many_segments_planned(gpu, dtype, d, hq, hkv, bs, batch):
+    """Planned calls of more than 64 segments (the one-stream merge, as at the benchmark shapes).
+
+    Lengths include empty sequences, single keys, block edges and one long sequence whose
+    segments split into hundreds of pieces (several merge chunks). Checked: the planned call
+    bit-identical to the unplanned one, three planned calls in a row identical, against
+    float64 with stale NaN rows planted, and the fused planned call equal to kv_append
+    followed by the unplanned decode, pools and outputs bit for bit."""
+    from engine import paged_ops
+
+    announce(f"planned decode, many segments {dtype} d={d} hq={hq} hkv={hkv} bs={bs} B={batch}")
+    rng = random.Random(batch + d)
+    lens = [0, 1, bs, bs + 1, 16, 17, 30000] + [rng.randint(1, 900) for _ in range(batch - 7)]
+    q, k_pool, v_pool, tables, bt, width = _random_case(dtype, batch, hq, hkv, d, bs, lens, seed=batch + 7 * d,
+                                                        stale=float("nan"))
+    qg, kg, vg = q.to(gpu), k_pool.to(gpu), v_pool.to(gpu)
+    bt_t = torch.from_numpy(bt).to(gpu)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=gpu)
+    plan = paged_ops.decode_plan(lens_t, bt_t, hq, hkv, d, bs, DTYPES[dtype], max_blocks=width)
+    assert plan is not None
+    out0 = paged_ops.paged_decode(qg, kg, vg, bt_t, lens_t, max_blocks=width)
+    outs = [paged_ops.paged_decode(qg, kg, vg, bt_t, lens_t, max_blocks=width, plan=plan) for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o, out0)
+    want = ref.attention_f64(values(q), values(k_pool), values(v_pool), tables, lens, bs)
+    got = values(out0)
+    assert np.isfinite(got).all()
+    assert attention_error(got, want, dtype) <= TOL[dtype]
+    # fused: the planned call against kv_append + the unplanned decode
+    g = torch.Generator().manual_seed(batch)
+    k_new = torch.randn(batch, hkv, d, generator=g).to(DTYPES[dtype]).to(gpu)
+    v_new = torch.randn(batch, hkv, d, generator=g).to(DTYPES[dtype]).to(gpu)
+    slots = torch.tensor([tables[b][(n - 1) // bs] * bs + (n - 1) % bs if n > 0 else -1 for b, n in enumerate(lens)],
+                         dtype=torch.int64, device=gpu)
+    ka, va, kb, vb = kg.clone(), vg.clone(), kg.clone(), vg.clone()
+    paged_ops.kv_append(ka, va, k_new, v_new, slots)
+    fa = paged_ops.paged_decode(qg, ka, va, bt_t, lens_t, max_blocks=width)
+    fb = paged_ops.paged_decode_append(qg, k_new, v_new, kb, vb, slots, bt_t, lens_t, max_blocks=width, plan=plan)
+    torch.cuda.synchronize()
+    # bit patterns: the planted NaN rows compare unequal as values
+    assert np.array_equal(storage(ka), storage(kb)) and np.array_equal(storage(va), storage(vb)), "pools differ"
+    assert torch.equal(fa, fb), "outputs differ"
+
+
 def test_paged_decode_large_logits_rescale(gpu):
     """Scores spanning hundreds of units exercise the lazy running-max rescale."""
     from engine import paged_ops
@@ -751,26 +799,29 @@ def test_planned_fused_decode_graph_replay_config3_padded_matches_oracle(gpu):
         _ = (q.float() * 2).sum().item()  # unrelated eager work between replays
 
 
-def test_mismatched_plan_fails_visibly(gpu):
+@pytest.mark.parametrize("batch", [4, 70])
+def test_mismatched_plan_fails_visibly(gpu, batch):
     """A plan made for another batch: the Python layer refuses it, and through the C ABI the
-    call writes NaN to every output row and leaves the pool unchanged (no silent garbage)."""
+    call writes NaN to every output row and leaves the pool unchanged (no silent garbage).
+    Batch 4 (8 segments) takes the two-stream merge with runs; batch 70 (140 segments) the
+    one-stream merge."""
     from engine import paged_ops
 
-    announce("decode with a plan of another batch size")
-    lens = [40, 700, 1300, 5]
-    q, k_pool, v_pool, tables, bt, width = _random_case("bfloat16", 4, 14, 2, 64, 16, lens, seed=23)
+    announce(f"decode with a plan of another batch size, B={batch}")
+    lens = ([40, 700, 1300, 5] * 18)[:batch]
+    q, k_pool, v_pool, tables, bt, width = _random_case("bfloat16", batch, 14, 2, 64, 16, lens, seed=23)
     qg, kg, vg = q.to(gpu), k_pool.to(gpu), v_pool.to(gpu)
     btg = torch.from_numpy(bt).to(gpu)
     cl = torch.tensor(lens, dtype=torch.int32, device=gpu)
     slots = torch.tensor([tables[i][(n - 1) // 16] * 16 + (n - 1) % 16 for i, n in enumerate(lens)],
                          dtype=torch.int64, device=gpu)
-    k_new = torch.randn(4, 2, 64, device=gpu).to(torch.bfloat16)
-    v_new = torch.randn(4, 2, 64, device=gpu).to(torch.bfloat16)
+    k_new = torch.randn(batch, 2, 64, device=gpu).to(torch.bfloat16)
+    v_new = torch.randn(batch, 2, 64, device=gpu).to(torch.bfloat16)
     lib = paged_ops._native.load()
-    need4 = lib.mip_paged_decode_plan_bytes(4, 14, 2, 64, 16, width, paged_ops.dtype_code(torch.bfloat16))
-    need3 = lib.mip_paged_decode_plan_bytes(3, 14, 2, 64, 16, width, paged_ops.dtype_code(torch.bfloat16))
+    need4 = lib.mip_paged_decode_plan_bytes(batch, 14, 2, 64, 16, width, paged_ops.dtype_code(torch.bfloat16))
+    need3 = lib.mip_paged_decode_plan_bytes(batch - 1, 14, 2, 64, 16, width, paged_ops.dtype_code(torch.bfloat16))
     buf = torch.zeros(-(-max(need4, need3) // 4), dtype=torch.int32, device=gpu)
-    paged_ops.decode_plan(cl[:3], btg[:3], 14, 2, 64, 16, torch.bfloat16, max_blocks=width, plan=buf)
+    paged_ops.decode_plan(cl[:-1], btg[:-1], 14, 2, 64, 16, torch.bfloat16, max_blocks=width, plan=buf)
     with pytest.raises(ValueError, match="plan was made for"):
         paged_ops.paged_decode_append(qg, k_new, v_new, kg, vg, slots, btg, cl, max_blocks=width, plan=buf)
     del buf._mip_plan_key  # reach the library as a caller of the C ABI would
