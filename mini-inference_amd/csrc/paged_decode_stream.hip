@@ -25,8 +25,9 @@
 //     tables and context lengths are read with scalar loads, and cross-lane sums use
 //     v_permlane{16,32}_swap, so nothing else in the loop touches LDS.
 //   * K and q rows are stored with their 16-byte chunks XOR-swizzled by row, so the 16 rows
-//     read by one ds_read_b128 hit distinct banks. V is stored plainly and read with gfx950's
-//     transposing ds_read_b64_tr_b16 (4 keys of one dim per lane, one read per 16 dims).
+//     read by one ds_read_b128 hit distinct banks. V rows are swizzled by an even XOR (whole
+//     32-byte segments) and read with gfx950's transposing ds_read_b64_tr_b16 (4 keys of one
+//     dim per lane, one read per 16 dims), so its rows too start in distinct banks.
 //
 // Tile arithmetic (lane l: row/head l%16, lane group l/16):
 //   S^T[16 keys x 16 heads] = K . Q^T        v_mfma_f32_16x16x32_{bf16,f16}, D/32 steps
@@ -84,6 +85,10 @@ struct Ring {
   static constexpr int KC = D / 32;
   static constexpr int MT = D / 16;
   static_assert(QI >= 1, "q block must fill at least one direct load");
+  // V row r keeps its 16-byte chunk c at c ^ vsw(r). The XOR is even, so each 32-byte segment a
+  // transposing read takes stays whole, and the 8 rows one 32-lane half of such a read touches
+  // start their segments in distinct banks (the layout of the prefill kernel's V tile).
+  static __device__ __forceinline__ int vsw(int r) { return CPR >= 16 ? 2 * (r & 7) : 2 * ((r + (r >> 2)) & 3); }
 };
 
 template <int N>
@@ -272,8 +277,15 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     q_addr[kc] = ring + R::Q_OFF + qrow * RB + ((c ^ (qrow & (CPR - 1))) * 16);
   }
   // V^T operand by transposing reads: lane i16 = 4k + r points at dims 4r .. 4r + 3 (+16 mt) of
-  // key 4 grp + k and receives dim 16 mt + i16 of keys 4 grp + 0..3.
-  const uint32_t v_addr = ring + R::V_OFF + (4 * grp + (i16 >> 2)) * RB + (i16 & 3) * 8;
+  // key 4 grp + k and receives dim 16 mt + i16 of keys 4 grp + 0..3. Segment mt of the lane's
+  // row sits at chunk (2 mt) ^ vsw(row).
+  uint32_t v_addr[MT];
+  {
+    const int vrow = 4 * grp + (i16 >> 2), vs = R::vsw(vrow);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      v_addr[mt] = ring + R::V_OFF + vrow * RB + (((2 * mt) ^ vs) * 16) + (i16 & 3) * 8;
+  }
   const int dma_r = lane / CPR, dma_pc = lane % CPR;
 
   uint32_t vmask[NS];  // per stage: bit r = key row r of the tile is a key of its segment
@@ -304,10 +316,10 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
       for (int j = 0; j < R::KI; ++j) {
         const int r = j * RPD + dma_r;
         const int64_t row = row0 + (r < nvalid ? r : 0);
-        const int lc = dma_pc ^ (r & (CPR - 1));
+        const int lc = dma_pc ^ (r & (CPR - 1)), vc = dma_pc ^ R::vsw(r);
         const bool fresh = r == nr;
         dma16_kv(fresh ? nk + lc * 16 : a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
-        dma16_kv(fresh ? nv + dma_pc * 16 : a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
+        dma16_kv(fresh ? nv + vc * 16 : a.v + row * RB + vc * 16, st + R::V_OFF + j * 1024);
       }
     } else {
       // Small blocks: every row looks its block up; rows that are not keys re-read the
@@ -332,10 +344,10 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
         const int bl = table[(tok < pL ? tok : tk0) >> a.log2_bs];
         const bool ok = tok < pL && bl >= 0 && bl < sa.ncb;
         const int64_t row = ok ? static_cast<int64_t>(bl * a.hkv + pkvh) * a.bs + (tok & (a.bs - 1)) : row_first;
-        const int lc = dma_pc ^ (r & (CPR - 1));
+        const int lc = dma_pc ^ (r & (CPR - 1)), vc = dma_pc ^ R::vsw(r);
         const bool fresh = ok && tok == pL - 1 && static_cast<int64_t>(bl) * a.bs + (tok & (a.bs - 1)) == new_slot;
         dma16_kv(fresh ? nk + lc * 16 : a.k + row * RB + lc * 16, st + R::K_OFF + j * 1024);
-        dma16_kv(fresh ? nv + dma_pc * 16 : a.v + row * RB + dma_pc * 16, st + R::V_OFF + j * 1024);
+        dma16_kv(fresh ? nv + vc * 16 : a.v + row * RB + vc * 16, st + R::V_OFF + j * 1024);
       }
     }
 #pragma unroll
@@ -380,7 +392,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
     if (vm) {
       static_for<0, MT>([&](auto mtc) {
         constexpr int mt = decltype(mtc)::value;
-        ve[mt] = lds_tr16<SO + 32 * mt>(v_addr);
+        ve[mt] = lds_tr16<SO>(v_addr[mt]);
       });
     }
     lgkm_wait();
@@ -583,8 +595,15 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
     q_addr[kc] = ring + R::Q_OFF + qrow * RB + ((c ^ (qrow & (CPR - 1))) * 16);
   }
   // V^T operand by transposing reads: lane i16 = 4k + r points at dims 4r .. 4r + 3 (+16 mt) of
-  // key 4 grp + k and receives dim 16 mt + i16 of keys 4 grp + 0..3.
-  const uint32_t v_addr = ring + R::V_OFF + (4 * grp + (i16 >> 2)) * RB + (i16 & 3) * 8;
+  // key 4 grp + k and receives dim 16 mt + i16 of keys 4 grp + 0..3. Segment mt of the lane's
+  // row sits at chunk (2 mt) ^ vsw(row).
+  uint32_t v_addr[MT];
+  {
+    const int vrow = 4 * grp + (i16 >> 2), vs = R::vsw(vrow);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      v_addr[mt] = ring + R::V_OFF + vrow * RB + (((2 * mt) ^ vs) * 16) + (i16 & 3) * 8;
+  }
   const int dma_r = lane / CPR, dma_pc = lane % CPR;
   // Lane offsets inside a tile's rows (row r < valid keys; other rows re-read row 0).
   uint32_t k_lane[R::KI], v_lane[R::KI];
@@ -594,7 +613,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
     const int r = j * RPD + dma_r;
     r_lane[j] = r;
     k_lane[j] = static_cast<uint32_t>(r * RB + ((dma_pc ^ (r & (CPR - 1))) * 16));
-    v_lane[j] = static_cast<uint32_t>(r * RB + dma_pc * 16);
+    v_lane[j] = static_cast<uint32_t>(r * RB + ((dma_pc ^ R::vsw(r)) * 16));
   }
   uint32_t q_lane[R::QI];
 #pragma unroll
@@ -650,7 +669,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
         const uint32_t ko = r < nvalid ? k_lane[j] : k_lane[j] - static_cast<uint32_t>(r * RB);
         const uint32_t vo = r < nvalid ? v_lane[j] : v_lane[j] - static_cast<uint32_t>(r * RB);
         dma16_kv(fresh ? nk + (k_lane[j] - r * RB) : kb + ko, st + R::K_OFF + j * 1024);
-        dma16_kv(fresh ? nv + dma_pc * 16 : vb + vo, st + R::V_OFF + j * 1024);
+        dma16_kv(fresh ? nv + (v_lane[j] - r * RB) : vb + vo, st + R::V_OFF + j * 1024);
       }
     } else {
 #pragma unroll
@@ -710,7 +729,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
     if (vm) {
       static_for<0, MT>([&](auto mtc) {
         constexpr int mt = decltype(mtc)::value;
-        ve[mt] = lds_tr16<SO + 32 * mt>(v_addr);
+        ve[mt] = lds_tr16<SO>(v_addr[mt]);
       });
     }
     lgkm_wait();
