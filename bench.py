@@ -460,19 +460,26 @@ def copy_measure(dev, iters: int = 40, sets: int = 8) -> dict:
     }
 
 
+PROBE_MODES = {"grid_stride": 0, "span_lds": 1, "span_lds_nt": 2}
+
+
 def hbm_ceiling(dev, nbytes: int, chunk: int = 2048, sets: int = 24, iters: int = 48,
-                grids: tuple[int, ...] = (1024, 2048, 4096, 8192)) -> dict:
+                grids: dict | None = None) -> dict:
     """What this GPU streams for ``nbytes`` (one decode call's algorithmic bytes): the library's
     read probe (``mip_hbm_read_probe``) over randomly placed ``chunk``-byte chunks of a 4 GiB
     buffer; over random chunks drawn from a window of twice the bytes, as one layer's K and V
     pools are read (a window per set, each of its chunks used once); and over one contiguous
-    run. Each cycles ``sets`` disjoint chunk sets so nothing is served from the 256 MB
-    last-level cache; the fastest of ``grids`` (workgroups of 256 threads) is reported. HIP
-    events."""
+    run. Each pattern is read three ways (grid-stride register loads; contiguous spans per
+    wavefront through an LDS ring of direct loads, the decode kernel's path; the same with the
+    nontemporal cache policy, as the decode kernel's K/V loads), each at a few grids
+    (workgroups of 256 threads), and cycles ``sets`` disjoint chunk sets so nothing is served
+    from the 256 MB last-level cache. The fastest launch of each pattern is reported, with the
+    best of each read path beside it. HIP events."""
     import torch
 
     from engine import _native
 
+    grids = grids or {"grid_stride": (512, 1024, 1536, 2048), "span_lds": (512, 768), "span_lds_nt": (512, 768)}
     lib = _native.load()
     pool_bytes = 4 << 30
     buf = torch.zeros(pool_bytes // 4, dtype=torch.int32, device=dev)
@@ -488,38 +495,47 @@ def hbm_ceiling(dev, nbytes: int, chunk: int = 2048, sets: int = 24, iters: int 
     windowed = [((i % nwin) * win + torch.randperm(win, generator=gen, device=dev)[:per]).to(torch.int32)
                 for i in range(sets)]
     seq = [torch.arange(i * per, (i + 1) * per, dtype=torch.int32, device=dev) for i in range(sets)]
-    sink = torch.empty(max(grids) * 256, dtype=torch.int32, device=dev)
+    sink = torch.empty(max(max(g) for g in grids.values()) * 256, dtype=torch.int32, device=dev)
     st = torch.cuda.current_stream(dev).cuda_stream
     out = {}
     for name, chunks in (("random_chunks", [ids[i] for i in range(sets)]), ("random_chunks_layer_window", windowed),
                          ("sequential", seq)):
-        by_grid = {}
-        for grid in grids:
-            args = [(buf.data_ptr(), pool_bytes, c.data_ptr(), per, chunk, sink.data_ptr(), grid, st) for c in chunks]
-            it = [0]
+        by_mode = {}
+        for mode, mode_grids in grids.items():
+            by_grid = {}
+            for grid in mode_grids:
+                args = [(buf.data_ptr(), pool_bytes, c.data_ptr(), per, chunk, sink.data_ptr(), grid, PROBE_MODES[mode],
+                         st) for c in chunks]
+                it = [0]
 
-            def call():
-                a = args[it[0] % sets]
-                it[0] += 1
-                rc = lib.mip_hbm_read_probe(*a)
-                if rc:
-                    _native.check(rc, "mip_hbm_read_probe")
+                def call():
+                    a = args[it[0] % sets]
+                    it[0] += 1
+                    rc = lib.mip_hbm_read_probe(*a)
+                    if rc:
+                        _native.check(rc, "mip_hbm_read_probe")
 
-            for _ in range(sets):
-                call()
-            torch.cuda.synchronize()
-            by_grid[grid] = time_loop(call, iters)
-        grid, t = min(by_grid.items(), key=lambda kv: kv[1])
+                for _ in range(sets):
+                    call()
+                torch.cuda.synchronize()
+                by_grid[grid] = time_loop(call, iters)
+            grid, t = min(by_grid.items(), key=lambda kv: kv[1])
+            by_mode[mode] = {"us": round(t * 1e6, 2), "grid": grid,
+                             "us_by_grid": {str(g): round(v * 1e6, 2) for g, v in by_grid.items()}}
+        mode = min(by_mode, key=lambda m: by_mode[m]["us"])
+        t = by_mode[mode]["us"] * 1e-6
         out[name] = {"us": round(t * 1e6, 2), "GBps": round(per * chunk / t / 1e9, 1),
-                     "frac": round(per * chunk / t / 1e9 / HBM_PEAK_GBPS, 4), "grid": grid,
-                     "us_by_grid": {str(g): round(v * 1e6, 2) for g, v in by_grid.items()}}
+                     "frac": round(per * chunk / t / 1e9 / HBM_PEAK_GBPS, 4), "mode": mode,
+                     "grid": by_mode[mode]["grid"], "by_mode": by_mode}
     del buf, ids, windowed, seq, sink
     torch.cuda.empty_cache()
-    out.update({"kernel": "hbm_read_probe_kernel", "bytes": per * chunk, "chunk_bytes": chunk,
+    out.update({"kernel": "hbm_read_probe_kernel / hbm_read_probe_ring_kernel", "bytes": per * chunk,
+                "chunk_bytes": chunk,
                 "workload": f"read {per * chunk} B as {per} randomly placed {chunk}-byte chunks of a 4 GiB buffer, "
                             f"as {per} random chunks of a {win * chunk}-byte window (one per set), and as one "
-                            f"contiguous run; {sets} disjoint sets cycled, the fastest of grids {list(grids)} x 256 "
-                            f"threads"})
+                            f"contiguous run; {sets} disjoint sets cycled; each by grid-stride register loads, by "
+                            f"contiguous spans per wavefront through an LDS ring of direct loads, and the same "
+                            f"with the nontemporal policy; the fastest launch reported"})
     return out
 
 
@@ -672,11 +688,11 @@ def main() -> int:
             hc["decode_call_frac_of_layer_window"] = round(achieved / hc["random_chunks_layer_window"]["GBps"], 4)
             result["hbm_ceiling"] = hc
             log(f"hbm probe: {hc['bytes']} B as random 2 KiB chunks {hc['random_chunks']['us']} us "
-                f"({hc['random_chunks']['GBps']} GB/s), within a layer-sized window "
+                f"({hc['random_chunks']['GBps']} GB/s, {hc['random_chunks']['mode']}), within a layer-sized window "
                 f"{hc['random_chunks_layer_window']['us']} us ({hc['random_chunks_layer_window']['GBps']} GB/s, the "
-                f"decode call reaches {hc['decode_call_frac_of_layer_window']:.1%} of it), sequential {hc['sequential']['us']} us "
-                f"({hc['sequential']['GBps']} GB/s); the decode call reaches "
-                f"{hc['decode_call_frac_of_random_chunks']:.1%} of the random-chunk rate")
+                f"decode call reaches {hc['decode_call_frac_of_layer_window']:.1%} of it), sequential "
+                f"{hc['sequential']['us']} us ({hc['sequential']['GBps']} GB/s, {hc['sequential']['mode']}); the decode "
+                f"call reaches {hc['decode_call_frac_of_random_chunks']:.1%} of the random-chunk rate")
         except Exception as exc:
             log(f"hbm probe failed: {exc!r}")
             result["hbm_ceiling"] = None
@@ -743,7 +759,7 @@ def main() -> int:
             if not args.no_probe:
                 # The same bytes through the read probe, as 8 KiB chunks (one block's K or V rows of
                 # one kv head at this shape); 4 disjoint sets of the 4 GiB buffer, cycled.
-                lh = hbm_ceiling(dev, lc["bytes_per_layer"], chunk=8192, sets=4, iters=12, grids=(2048, 4096, 8192))
+                lh = hbm_ceiling(dev, lc["bytes_per_layer"], chunk=8192, sets=4, iters=12)
                 lh["decode_call_frac_of_layer_window"] = round(lc["achieved"] / lh["random_chunks_layer_window"]["GBps"], 4)
                 lc["hbm_ceiling"] = lh
                 log(f"long-context hbm probe: {lh['bytes']} B as random 8 KiB chunks {lh['random_chunks']['us']} us "

@@ -83,7 +83,7 @@ _SIGNATURES = {
     ),
     "mip_copy_blocks": (_c.c_int, [_vp, _vp, _vp, _i32, _i32, _i64, _i64, _vp]),
     "mip_copy_blocks_host": (_c.c_int, [_vp, _vp, _vp, _i32, _i32, _i64, _i64, _vp]),
-    "mip_hbm_read_probe": (_c.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _i32, _vp]),
+    "mip_hbm_read_probe": (_c.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _i32, _i32, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -389,6 +389,20 @@ def test_abi_host_checks_return_before_launch(lib):
         assert cp(16, 16, 16, 3, 1 << 23, 100, 16, None) == E      # one pair alone exceeds a launch's grid
 
 
+def test_probe_argument_checks(lib):
+    """mip_hbm_read_probe refuses bad arguments before it launches anything: an unknown read
+    path, chunk sizes that are not whole KiB, and (the LDS-ring paths) a wavefront span of more
+    than the 128 chunk ids a wavefront holds."""
+    E, OK = _native.MIP_EINVAL, _native.MIP_OK
+    probe = lib.mip_hbm_read_probe
+    assert probe(16, 1 << 30, 16, 0, 2048, 16, 1, 0, None) == OK        # no chunks: nothing to read
+    assert probe(16, 1 << 30, 16, 10, 2048, 16, 1, 3, None) == E        # unknown read path
+    assert probe(16, 1 << 30, 16, 10, 1000, 16, 1, 0, None) == E        # not a multiple of 1 KiB
+    assert probe(None, 1 << 30, 16, 10, 2048, 16, 1, 0, None) == E      # null base
+    for mode in (1, 2):
+        assert probe(16, 1 << 30, 16, 1000, 2048, 16, 1, mode, None) == E  # 250 chunks per wavefront
+
+
 def test_decode_algo_setting(lib):
     """mip_set_decode_algo: returns the previous setting, refuses unknown values, host-only."""
     prev = _native.set_decode_algo("valu")
