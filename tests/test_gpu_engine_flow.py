@@ -28,8 +28,9 @@ pytestmark = pytest.mark.gpu
 
 BS = 16
 # Relative bound on |engine - alone| / max |logit|: the two runs batch the GEMMs differently
-# and, in bf16, round K/V and activations at different batch shapes.
-REL_TOL = {torch.float32: 1e-4, torch.bfloat16: 4e-2}
+# and, in bf16, round K/V and activations at different batch shapes (measured: fp32 9.7e-7,
+# bf16 7.1e-3 with a roomy pool and 9.0e-3 with preemption).
+REL_TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
 
 
 @dataclass
