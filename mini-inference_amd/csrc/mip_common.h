@@ -69,6 +69,23 @@ __device__ __forceinline__ int64_t load_uniform_i64(const int64_t* p) {
   return *(const __attribute__((address_space(4))) int64_t*)(p);
 }
 
+// A vector load issued where it is written. A relaxed atomic load is not sunk into the branch
+// that uses it and not reordered behind another one, so a group of them written back to back
+// goes out back to back and costs one memory round trip, however its values are tested
+// afterwards. (Plain loads of a prologue were sunk past an early-exit test and issued one
+// round trip after another.) The atomic is wavefront-scope: a plain global_load.
+__device__ __forceinline__ uint64_t load_now_u64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+
+// The two 32-bit halves of a wave-uniform 64-bit value, in scalar registers.
+__device__ __forceinline__ int uniform_lo(uint64_t x) {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(x)));
+}
+__device__ __forceinline__ int uniform_hi(uint64_t x) {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(x >> 32)));
+}
+
 __host__ __device__ constexpr int ilog2_exact(int x) { return x <= 1 ? 0 : 1 + ilog2_exact(x >> 1); }
 
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }

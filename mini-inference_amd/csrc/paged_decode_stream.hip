@@ -567,15 +567,27 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
   // latencies overlap. (The wavefront record of a wavefront past W is inside the plan too.)
   // This wavefront's descriptor slots start at a fixed place, so its first 64 descriptors
   // are read together with its range instead of after it.
-  const uint2* tdesc = reinterpret_cast<const uint2*>(plan + sa.plan_tile_off) +
-                       static_cast<int64_t>(gw) * sa.plan_wave_cap;
-  const int pw = load_uniform_i32(plan + 1), pb = load_uniform_i32(plan + 2), ph = load_uniform_i32(plan + 3);
-  const int pt = load_uniform_i32(plan + kPlanTileOffWord), pc = load_uniform_i32(plan + kPlanWaveCapWord);
-  const int lo = load_uniform_i32(plan + kPlanHeader + kPlanWave * gw);
-  const int hi = load_uniform_i32(plan + kPlanHeader + kPlanWave * gw + 1);
-  uint2 dv = tdesc[lane];
+  // The header's word pairs, the wavefront record and one descriptor per lane go out as one
+  // group of loads (load_now_u64: the plan is 8-byte aligned, the record and descriptors sit
+  // at even word offsets), so the start-up waits one round trip for all of them.
+  const uint64_t* tdesc = reinterpret_cast<const uint64_t*>(plan + sa.plan_tile_off) +
+                          static_cast<int64_t>(gw) * sa.plan_wave_cap;
+  const uint64_t* plan64 = reinterpret_cast<const uint64_t*>(plan);
+  const uint64_t h01 = load_now_u64(plan64 + 0);  // T, W
+  const uint64_t h23 = load_now_u64(plan64 + 1);  // batch, kv heads
+  const uint64_t h45 = load_now_u64(plan64 + 2);  // descriptor offset, segment-record offset
+  const uint64_t h67 = load_now_u64(plan64 + 3);  // descriptor slots per wavefront, 0
+  const uint64_t wr = load_now_u64(plan64 + (kPlanHeader + kPlanWave * gw) / 2);
+  const uint64_t d64 = load_now_u64(tdesc + lane);
+  static_assert(kPlanHeader % 2 == 0 && kPlanWave == 2 && kPlanTileOffWord == 4 && kPlanWaveCapWord == 6,
+                "plan header words are read in 8-byte pairs");
+  const int pw = uniform_hi(h01), pb = uniform_lo(h23), ph = uniform_hi(h23);
+  const int pt = uniform_lo(h45), pc = uniform_lo(h67);
+  const int lo = uniform_lo(wr), hi = uniform_hi(wr);
+  uint2 dv = make_uint2(static_cast<uint32_t>(d64), static_cast<uint32_t>(d64 >> 32));
   // A plan made for another batch, kv-head count or layout would index past this call's tensors.
-  if (pb != sa.batch || ph != a.hkv || pt != sa.plan_tile_off || pc != sa.plan_wave_cap || gw >= pw || lo >= hi)
+  if ((pb != sa.batch) | (ph != a.hkv) | (pt != sa.plan_tile_off) | (pc != sa.plan_wave_cap) | (gw >= pw) |
+      (lo >= hi))
     return;
 
   // ---- descriptors of tiles cbase .. cbase + 63 in registers (lane j holds tile cbase + j).
@@ -635,7 +647,7 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
     if (x >= hi) return;
     if (x - cbase >= kWave) {  // next 64 descriptors (long ranges only; drains the loads in flight)
       cbase = x;
-      dv = x + lane < hi ? tdesc[x - lo + lane] : make_uint2(kTileNoRow, 0u);
+      dv = x + lane < hi ? __builtin_bit_cast(uint2, tdesc[x - lo + lane]) : make_uint2(kTileNoRow, 0u);
     }
     const uint32_t row0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(dv.x), x - cbase));
     uint32_t meta = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(dv.y), x - cbase));
@@ -889,32 +901,63 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
   const AppendRows& ap = sa.app;
   constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
   const bool app_lane = FUSED && z == 0 && threadIdx.x < 2 * CPR;
+  // Every load of the prologue (the new token's slot, its rows, the plan's header and this
+  // segment's descriptor) is issued before any of them is tested, so together they cost one
+  // memory round trip before the records are read. The row source does not depend on the
+  // slot; only the store does. They are vector loads (every lane the same address): a wait
+  // for the scalar loads of the kernel arguments would also wait for scalar loads of these.
+  int64_t slot = -1;
+  if constexpr (FUSED) slot = __builtin_nontemporal_load(ap.slots + b);
+  int pb = 0, ph = 0, ps = 0, sd0 = 0, sd1 = 0, sd2 = 0, sd3 = 0;
+  if constexpr (PLANNED) {
+    const int32_t* sd = sa.plan + sa.plan_seg_off + (static_cast<int64_t>(b) * a.hkv + kvh) * kPlanSeg;
+    pb = __builtin_nontemporal_load(sa.plan + 2);
+    ph = __builtin_nontemporal_load(sa.plan + 3);
+    ps = __builtin_nontemporal_load(sa.plan + kPlanSegOffWord);
+    sd0 = __builtin_nontemporal_load(sd + 0);
+    sd1 = __builtin_nontemporal_load(sd + 1);
+    sd2 = __builtin_nontemporal_load(sd + 2);
+    sd3 = __builtin_nontemporal_load(sd + 3);
+  }
+  if constexpr (FUSED) {
+    slot = static_cast<int64_t>(
+        (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(slot >> 32))))
+         << 32) |
+        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(slot))));
+  }
+  if constexpr (PLANNED) {
+    pb = __builtin_amdgcn_readfirstlane(pb);
+    ph = __builtin_amdgcn_readfirstlane(ph);
+    ps = __builtin_amdgcn_readfirstlane(ps);
+    sd0 = __builtin_amdgcn_readfirstlane(sd0);
+    sd1 = __builtin_amdgcn_readfirstlane(sd1);
+    sd2 = __builtin_amdgcn_readfirstlane(sd2);
+    sd3 = __builtin_amdgcn_readfirstlane(sd3);
+  }
   uint4 app_row = make_uint4(0u, 0u, 0u, 0u);
-  char* app_dst = nullptr;
   if (app_lane) {
     const int side = threadIdx.x / CPR, c = threadIdx.x % CPR;
-    const int64_t slot = ap.slots[b];
-    if (slot >= 0 && slot < a.ncb * a.bs) {
-      const char* src = side ? ap.v + static_cast<int64_t>(b) * ap.v_st + static_cast<int64_t>(kvh) * ap.v_sh
-                             : ap.k + static_cast<int64_t>(b) * ap.k_st + static_cast<int64_t>(kvh) * ap.k_sh;
-      app_dst = (side ? ap.v_cache : ap.k_cache) +
-                (((slot >> a.log2_bs) * a.hkv + kvh) * a.bs + (slot & (a.bs - 1))) * (D * 2) + c * 16;
-      app_row = *reinterpret_cast<const uint4*>(src + c * 16);
-    }
+    const char* src = side ? ap.v + static_cast<int64_t>(b) * ap.v_st + static_cast<int64_t>(kvh) * ap.v_sh
+                           : ap.k + static_cast<int64_t>(b) * ap.k_st + static_cast<int64_t>(kvh) * ap.k_sh;
+    app_row = *reinterpret_cast<const uint4*>(src + c * 16);
+  }
+  char* app_dst = nullptr;
+  if (app_lane && slot >= 0 && slot < a.ncb * a.bs) {
+    const int side = threadIdx.x / CPR, c = threadIdx.x % CPR;
+    app_dst = (side ? ap.v_cache : ap.k_cache) +
+              (((slot >> a.log2_bs) * a.hkv + kvh) * a.bs + (slot & (a.bs - 1))) * (D * 2) + c * 16;
   }
   int L, gw_lo, gw_hi;
   bool lo_split;
   if constexpr (PLANNED) {
-    const int32_t* sd = sa.plan + sa.plan_seg_off + (static_cast<int64_t>(b) * a.hkv + kvh) * kPlanSeg;
-    const int pb = load_uniform_i32(sa.plan + 2), ph = load_uniform_i32(sa.plan + 3);
-    const int ps = load_uniform_i32(sa.plan + kPlanSegOffWord);
-    gw_lo = load_uniform_i32(sd + 0);
-    gw_hi = gw_lo + load_uniform_i32(sd + 1) - 1;
-    lo_split = load_uniform_i32(sd + 2) != 0;
-    L = load_uniform_i32(sd + 3);
+    gw_lo = sd0;
+    gw_hi = sd0 + sd1 - 1;
+    lo_split = sd2 != 0;
+    L = sd3;
     // A plan of another shape: the main kernel computed nothing. The call fails visibly:
     // NaN in every output row of this segment, and the pool is left as it was (no append).
-    if (pb != sa.batch || ph != a.hkv || ps != sa.plan_seg_off || gw_lo < 0 || gw_hi >= sa.tw) {
+    // (Bitwise ors: one test of all the words, after all of them have arrived.)
+    if ((pb != sa.batch) | (ph != a.hkv) | (ps != sa.plan_seg_off) | (gw_lo < 0) | (gw_hi >= sa.tw)) {
       if (z == 0)
         for (int i = threadIdx.x; i < G * D; i += blockDim.x)
           out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + i / D) * a.out_sh + i % D] =
@@ -925,12 +968,18 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
     L = a.lens[b];
     L = L < cap ? L : cap;
   }
-  if (app_dst) *reinterpret_cast<uint4*>(app_dst) = app_row;
+  // The new rows are stored on each way out of the kernel (the workgroup z = 0 of a segment
+  // takes one of them), after the record loads are issued: a store of the rows before those
+  // loads would make them wait for the rows' load as well.
+  auto store_app = [&]() __attribute__((always_inline)) {
+    if (app_dst) *reinterpret_cast<uint4*>(app_dst) = app_row;
+  };
   if (L <= 0) {
     if (z == 0)
       for (int i = threadIdx.x; i < G * D; i += blockDim.x)
         out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + i / D) * a.out_sh + i % D] =
             from_f32<DT>(0.0f);
+    store_app();
     return;
   }
   if constexpr (!PLANNED) {
@@ -943,7 +992,10 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
     gw_hi = static_cast<int>(((e1 + 1) * tw - 1) / total);
     lo_split = static_cast<int64_t>(gw_lo) * total / tw < s0;
   }
-  if (gw_lo >= gw_hi) return;  // one wavefront held the whole segment and wrote it
+  if (gw_lo >= gw_hi) {  // one wavefront held the whole segment and wrote it
+    store_app();
+    return;
+  }
   const int R = gw_hi - gw_lo + 1;
   // A segment of more than one round of chunks, with Z > 1, is cut into Z runs of consecutive
   // pieces [p0, p0 + np), one per workgroup z; each leaves its state in a second-level record
@@ -1094,6 +1146,7 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
         }
       }
     }
+    store_app();
     return;
   }
 #pragma unroll
@@ -1109,6 +1162,7 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
       o[3] = from_f32<DT>(acc[j].w * inv);
     }
   }
+  store_app();
 }
 
 // Second level of the merge for calls with few segments: combines the kStreamParts run
