@@ -38,6 +38,14 @@ HIPCC_FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
 ]
+# Per-source flags. The stream decode kernels take their plan pointer and word offsets as
+# leading scalar arguments; preloading them into scalar registers at wave launch (gfx950
+# kernel-argument preloading) lets a kernel's first plan reads go out without waiting for a
+# load of its arguments. Code objects keep a fallback that loads them where the firmware does
+# not preload.
+FILE_FLAGS = {
+    "paged_decode_stream.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=3"],
+}
 
 
 def hipcc() -> str:
@@ -49,7 +57,7 @@ def hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

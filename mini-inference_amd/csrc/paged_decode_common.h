@@ -110,6 +110,10 @@ struct StreamArgs {
   int tw;          // wavefronts in the grid
   int min_tiles;   // fewest tiles an active wavefront takes
   int max_pieces;  // most wavefronts per segment, on average (caps W at segments * max_pieces)
+  // The records sit next to the fields the merge kernel reads first (batch, tw), in the same
+  // 64-byte line of the kernel arguments, so reading them costs no further argument load.
+  int rec_stride;  // floats per record: m[16] | l[16] | acc[group][D]
+  float* ws_rec;   // [tw][2][rec_stride]
   AppendRows app;
   const int32_t* plan;  // stream work plan for these context lengths (nullptr: derive it in-kernel)
   // 32-bit copies of the 64-bit strides / sizes of DecodeArgs (the host checks they fit), so
@@ -118,9 +122,7 @@ struct StreamArgs {
   uint32_t nrows;  // rows of one layer's pool (num_cache_blocks * kv heads * block size)
   int32_t plan_seg_off, plan_tile_off;  // word offsets of the plan's segment records / tile descriptors
   int32_t plan_wave_cap;                // descriptor slots per wavefront in the plan
-  int rec_stride;  // floats per record: m[16] | l[16] | acc[group][D]
   int* ws_prefix;  // [batch + 1] tile prefix over sequences (written by workgroup 0)
-  float* ws_rec;   // [tw][2][rec_stride]
   // Calls with few segments: the merge cuts a segment of many pieces into `parts` runs (one
   // workgroup each) and leaves their states here, [batch * kv heads][parts][rec_stride], for
   // the fold kernel. parts = 1: the merge combines every segment whole.

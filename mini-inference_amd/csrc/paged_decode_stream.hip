@@ -171,7 +171,7 @@ __device__ __forceinline__ bool static_all(F&& f) {
 }
 
 template <int DT, int D, int QR, int NS, bool FUSED>
-__global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa) {
+__global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(const int32_t*, int32_t, int32_t, StreamArgs sa) {
   using R = Ring<D, QR>;
   using Ops = MfmaOps<DT>;
   using S = typename Elem<DT>::S;
@@ -547,7 +547,9 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream(StreamArgs sa
 // does no block-table lookups and no cursor arithmetic. A wavefront holds up to 64 of its
 // descriptors in registers (one per lane, loaded once) and takes each with a lane read.
 template <int DT, int D, int QR, int NS, bool FUSED>
-__global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamArgs sa) {
+__global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(const int32_t* __restrict__ plan,
+                                                                        int32_t plan_tile_off, int32_t plan_wave_cap,
+                                                                        StreamArgs sa) {
   using R = Ring<D, QR>;
   using Ops = MfmaOps<DT>;
   using S = typename Elem<DT>::S;
@@ -562,7 +564,6 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
   const int i16 = lane & 15, grp = lane >> 4;
   const AppendRows& ap = sa.app;
   const int gw = blockIdx.x * kSW + w;
-  const int32_t* plan = sa.plan;
   // All plan words this wavefront needs are read before any of them is tested, so their
   // latencies overlap. (The wavefront record of a wavefront past W is inside the plan too.)
   // This wavefront's descriptor slots start at a fixed place, so its first 64 descriptors
@@ -570,8 +571,8 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
   // The header's word pairs, the wavefront record and one descriptor per lane go out as one
   // group of loads (load_now_u64: the plan is 8-byte aligned, the record and descriptors sit
   // at even word offsets), so the start-up waits one round trip for all of them.
-  const uint64_t* tdesc = reinterpret_cast<const uint64_t*>(plan + sa.plan_tile_off) +
-                          static_cast<int64_t>(gw) * sa.plan_wave_cap;
+  const uint64_t* tdesc = reinterpret_cast<const uint64_t*>(plan + plan_tile_off) +
+                          static_cast<int64_t>(gw) * plan_wave_cap;
   const uint64_t* plan64 = reinterpret_cast<const uint64_t*>(plan);
   const uint64_t h01 = load_now_u64(plan64 + 0);  // T, W
   const uint64_t h23 = load_now_u64(plan64 + 1);  // batch, kv heads
@@ -585,8 +586,13 @@ __global__ __launch_bounds__(kSW * kWave) void paged_decode_stream_tiles(StreamA
   const int pt = uniform_lo(h45), pc = uniform_lo(h67);
   const int lo = uniform_lo(wr), hi = uniform_hi(wr);
   uint2 dv = make_uint2(static_cast<uint32_t>(d64), static_cast<uint32_t>(d64 >> 32));
+  // One field from each 64-byte line of the argument block the first tiles use (q, the pool,
+  // the scale, batch and kv heads, the pool's row count and q strides): their loads go out
+  // now, beside the plan reads, instead of each line costing one more round trip before the
+  // first K/V loads and the first tile's arithmetic.
+  asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.scale_log2), "s"(sa.batch), "s"(sa.nrows));
   // A plan made for another batch, kv-head count or layout would index past this call's tensors.
-  if ((pb != sa.batch) | (ph != a.hkv) | (pt != sa.plan_tile_off) | (pc != sa.plan_wave_cap) | (gw >= pw) |
+  if ((pb != sa.batch) | (ph != a.hkv) | (pt != plan_tile_off) | (pc != plan_wave_cap) | (gw >= pw) |
       (lo >= hi))
     return;
 
@@ -884,7 +890,9 @@ constexpr int kStreamParts = 16;
 // segments), a segment of more than NSTR chunks is cut into runs of consecutive pieces, one
 // workgroup each, whose states paged_decode_stream_fold combines.
 template <int DT, int D, bool FUSED, bool PLANNED, int NSTR>
-__global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamArgs sa) {
+__global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const int32_t* __restrict__ plan,
+                                                                       int32_t plan_seg_off, int32_t hkv,
+                                                                       StreamArgs sa) {
   using S = typename Elem<DT>::S;
   const int64_t REC = sa.rec_stride;
   const DecodeArgs& a = sa.a;
@@ -901,52 +909,42 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
   const AppendRows& ap = sa.app;
   constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
   const bool app_lane = FUSED && z == 0 && threadIdx.x < 2 * CPR;
-  // Every load of the prologue (the new token's slot, its rows, the plan's header and this
-  // segment's descriptor) is issued before any of them is tested, so together they cost one
-  // memory round trip before the records are read. The row source does not depend on the
-  // slot; only the store does. They are vector loads (every lane the same address): a wait
-  // for the scalar loads of the kernel arguments would also wait for scalar loads of these.
-  int64_t slot = -1;
-  if constexpr (FUSED) slot = __builtin_nontemporal_load(ap.slots + b);
+  // The plan's header and this segment's descriptor are read first, from the preloaded plan
+  // pointer and by vector loads issued as one group (load_now_u64), so the records are read
+  // one round trip after the start: the kernel arguments arrive in parallel. The new token's
+  // slot and rows are needed only by the store at the end; the row source does not depend on
+  // the slot.
   int pb = 0, ph = 0, ps = 0, sd0 = 0, sd1 = 0, sd2 = 0, sd3 = 0;
   if constexpr (PLANNED) {
-    const int32_t* sd = sa.plan + sa.plan_seg_off + (static_cast<int64_t>(b) * a.hkv + kvh) * kPlanSeg;
-    pb = __builtin_nontemporal_load(sa.plan + 2);
-    ph = __builtin_nontemporal_load(sa.plan + 3);
-    ps = __builtin_nontemporal_load(sa.plan + kPlanSegOffWord);
-    sd0 = __builtin_nontemporal_load(sd + 0);
-    sd1 = __builtin_nontemporal_load(sd + 1);
-    sd2 = __builtin_nontemporal_load(sd + 2);
-    sd3 = __builtin_nontemporal_load(sd + 3);
+    // The plan is 8-byte aligned and the segment records start at an even word.
+    static_assert(kPlanSegOffWord == 5 && kPlanSeg == 4, "plan words are read in 8-byte pairs");
+    const uint64_t* p64 = reinterpret_cast<const uint64_t*>(plan);
+    const uint64_t* sd = reinterpret_cast<const uint64_t*>(plan + plan_seg_off) + (static_cast<int64_t>(b) * hkv + kvh) * 2;
+    const uint64_t h23 = load_now_u64(p64 + 1), h45 = load_now_u64(p64 + 2);
+    const uint64_t s01 = load_now_u64(sd), s23 = load_now_u64(sd + 1);
+    pb = uniform_lo(h23);
+    ph = uniform_hi(h23);
+    ps = uniform_hi(h45);
+    sd0 = uniform_lo(s01);
+    sd1 = uniform_hi(s01);
+    sd2 = uniform_lo(s23);
+    sd3 = uniform_hi(s23);
   }
-  if constexpr (FUSED) {
-    slot = static_cast<int64_t>(
-        (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(slot >> 32))))
-         << 32) |
-        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(slot))));
-  }
-  if constexpr (PLANNED) {
-    pb = __builtin_amdgcn_readfirstlane(pb);
-    ph = __builtin_amdgcn_readfirstlane(ph);
-    ps = __builtin_amdgcn_readfirstlane(ps);
-    sd0 = __builtin_amdgcn_readfirstlane(sd0);
-    sd1 = __builtin_amdgcn_readfirstlane(sd1);
-    sd2 = __builtin_amdgcn_readfirstlane(sd2);
-    sd3 = __builtin_amdgcn_readfirstlane(sd3);
-  }
+  // The slot is loaded by the append lanes only, as a vector load: a uniform load would be
+  // moved to a scalar register (and waited for) at once, and a scalar load would make the
+  // next wait for the kernel arguments wait for it as well. Only the store at the end reads it.
+  uint64_t slot_raw = ~0ull;
   uint4 app_row = make_uint4(0u, 0u, 0u, 0u);
   if (app_lane) {
+    slot_raw = load_now_u64(reinterpret_cast<const uint64_t*>(ap.slots) + b);
     const int side = threadIdx.x / CPR, c = threadIdx.x % CPR;
     const char* src = side ? ap.v + static_cast<int64_t>(b) * ap.v_st + static_cast<int64_t>(kvh) * ap.v_sh
                            : ap.k + static_cast<int64_t>(b) * ap.k_st + static_cast<int64_t>(kvh) * ap.k_sh;
     app_row = *reinterpret_cast<const uint4*>(src + c * 16);
   }
-  char* app_dst = nullptr;
-  if (app_lane && slot >= 0 && slot < a.ncb * a.bs) {
-    const int side = threadIdx.x / CPR, c = threadIdx.x % CPR;
-    app_dst = (side ? ap.v_cache : ap.k_cache) +
-              (((slot >> a.log2_bs) * a.hkv + kvh) * a.bs + (slot & (a.bs - 1))) * (D * 2) + c * 16;
-  }
+  // The pool geometry the store at the end needs sits in another line of the kernel arguments:
+  // read it now, with the rest, rather than one argument load before the kernel can end.
+  if constexpr (FUSED) asm volatile("" ::"s"(a.ncb), "s"(a.bs), "s"(a.log2_bs), "s"(a.hkv));
   int L, gw_lo, gw_hi;
   bool lo_split;
   if constexpr (PLANNED) {
@@ -957,7 +955,7 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
     // A plan of another shape: the main kernel computed nothing. The call fails visibly:
     // NaN in every output row of this segment, and the pool is left as it was (no append).
     // (Bitwise ors: one test of all the words, after all of them have arrived.)
-    if ((pb != sa.batch) | (ph != a.hkv) | (ps != sa.plan_seg_off) | (gw_lo < 0) | (gw_hi >= sa.tw)) {
+    if ((pb != sa.batch) | (ph != hkv) | (ps != plan_seg_off) | (gw_lo < 0) | (gw_hi >= sa.tw)) {
       if (z == 0)
         for (int i = threadIdx.x; i < G * D; i += blockDim.x)
           out_base[static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + i / D) * a.out_sh + i % D] =
@@ -972,7 +970,13 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
   // takes one of them), after the record loads are issued: a store of the rows before those
   // loads would make them wait for the rows' load as well.
   auto store_app = [&]() __attribute__((always_inline)) {
-    if (app_dst) *reinterpret_cast<uint4*>(app_dst) = app_row;
+    const int64_t slot = static_cast<int64_t>(slot_raw);
+    if (app_lane && slot >= 0 && slot < a.ncb * a.bs) {
+      const int side = threadIdx.x / CPR, c = threadIdx.x % CPR;
+      char* dst = (side ? ap.v_cache : ap.k_cache) +
+                  (((slot >> a.log2_bs) * a.hkv + kvh) * a.bs + (slot & (a.bs - 1))) * (D * 2) + c * 16;
+      *reinterpret_cast<uint4*>(dst) = app_row;
+    }
   };
   if (L <= 0) {
     if (z == 0)
@@ -1169,7 +1173,7 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(StreamAr
 // states the merge left for every parted segment, in run order with weights exp2(m_z - M),
 // M the largest m_z. Grid (kv heads, batch); segments the merge combined whole are skipped.
 template <int DT, int D, bool PLANNED>
-__global__ __launch_bounds__(256) void paged_decode_stream_fold(StreamArgs sa) {
+__global__ __launch_bounds__(256) void paged_decode_stream_fold(const int32_t*, int32_t, int32_t, StreamArgs sa) {
   using S = typename Elem<DT>::S;
   const int64_t REC = sa.rec_stride;
   const DecodeArgs& a = sa.a;
@@ -1357,7 +1361,11 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArg
   }
 }
 
-using StreamFn = void (*)(StreamArgs);
+// Every stream kernel takes the plan pointer and two of its word offsets ahead of the argument
+// block: the build preloads these leading scalar arguments into scalar registers (gfx950
+// kernel-argument preloading), so a planned kernel issues its first plan reads without first
+// waiting for a load of its arguments. Kernels that do not use them ignore them.
+using StreamFn = void (*)(const int32_t*, int32_t, int32_t, StreamArgs);
 
 struct StreamPick {
   StreamFn main[2][2] = {};   // [fused: with the step's K/V append][planned: from a work plan]
@@ -1515,13 +1523,17 @@ int stream_launch(const StreamConfig& cfg, const StreamArgs& sa_in, int dtype, i
   sa.max_pieces = stream_max_pieces(static_cast<int64_t>(batch) * num_kv_heads);
   sa.rec_stride = static_cast<int>(cfg.rec_floats);
   const int fused = sa.app.slots != nullptr, planned = sa.plan != nullptr;
-  hipLaunchKernelGGL(p.main[fused][planned], dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa);
+  hipLaunchKernelGGL(p.main[fused][planned], dim3(cfg.grid), dim3(kSW * kWave), cfg.lds_bytes, stream, sa.plan,
+                     sa.plan_tile_off, sa.plan_wave_cap, sa);
   const int64_t segments = static_cast<int64_t>(batch) * num_kv_heads;
   const int wide = stream_wide_merge(segments);
   sa.parts = stream_merge_parts(segments);
   hipLaunchKernelGGL(p.merge[fused][planned][wide], dim3(num_kv_heads, batch, sa.parts),
-                     dim3(wide ? 256 * kWideMergeStreams : 256), 0, stream, sa);
-  if (sa.parts > 1) hipLaunchKernelGGL(p.fold[planned], dim3(num_kv_heads, batch), dim3(256), 0, stream, sa);
+                     dim3(wide ? 256 * kWideMergeStreams : 256), 0, stream, sa.plan, sa.plan_seg_off, num_kv_heads,
+                     sa);
+  if (sa.parts > 1)
+    hipLaunchKernelGGL(p.fold[planned], dim3(num_kv_heads, batch), dim3(256), 0, stream, sa.plan, sa.plan_seg_off, 0,
+                       sa);
   return static_cast<int>(hipGetLastError());
 }
 
