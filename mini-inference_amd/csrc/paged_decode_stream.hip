@@ -1022,15 +1022,13 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
   };
   // Passes over chunks of 16 records with an online maximum per row. Every thread owns up
   // to two quads of four output columns of one row; the quads' partial sums of a chunk are
-  // loaded together with the chunk's (m, l) pairs, so a chunk costs one memory round trip.
+  // loaded together with the row's (m, l) pairs, so a chunk costs one memory round trip.
   // Stream str takes chunks str, str + NSTR, ... (a round count uniform over the workgroup,
-  // so every thread reaches every barrier).
+  // so every thread reaches the barrier of the stream fold below).
   constexpr int kRC = kMergeChunk;
   constexpr int Q = D / 4;  // column quads per row
-  __shared__ float s_m[NSTR][kRC][16];
-  __shared__ float s_l[NSTR][kRC][16];
   const int str = NSTR > 1 ? static_cast<int>(threadIdx.x) / 256 : 0;
-  const int t = NSTR > 1 ? static_cast<int>(threadIdx.x) % 256 : static_cast<int>(threadIdx.x), tg = t & 15, tr = t >> 4;
+  const int t = NSTR > 1 ? static_cast<int>(threadIdx.x) % 256 : static_cast<int>(threadIdx.x);
   const int nq = G * Q;  // quads per (kv head, sequence): at most 512
   const int nj = nq > 256 ? 2 : 1;
   float4 acc[2];
@@ -1042,10 +1040,17 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
     lrun[j] = 0.0f;
   }
   const int rounds = ((np + kRC - 1) / kRC + NSTR - 1) / NSTR;
-  for (int rd = 0; rd < rounds; ++rd) {
+  // One round as a function, called for the first round outside the loop over the others: in
+  // a loop the compiler waits before each load for the same registers' load of the previous
+  // round, which serialises a chunk's loads into one round trip per record.
+  auto round = [&](int rd) __attribute__((always_inline)) {
     const int c0 = p0 + (rd * NSTR + str) * kRC;  // first piece of this stream's chunk
     const int nr = c0 >= p0 + np ? 0 : (p0 + np - c0 < kRC ? p0 + np - c0 : kRC);  // 0: no chunk this round
+    // Each thread loads its own row's (m, l) pair of every record of the chunk beside the
+    // record's partial sums, so the chunk is folded in registers right after its one round
+    // trip (no exchange through LDS, no barrier). Records are read once: nontemporal loads.
     float4 v[2][kRC];
+    float mk[2][kRC], lk[2][kRC];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int qd = t + 256 * j;
@@ -1054,49 +1059,43 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
 #pragma unroll
         for (int k = 0; k < kRC; ++k)
           if (k < nr) {
-            // Records are read once: nontemporal loads (0.3 us less per config-3 call).
-            const f32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(rec_of(c0 + k) + 32 + g * D + col));
+            const float* rec = rec_of(c0 + k);
+            const f32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(rec + 32 + g * D + col));
             v[j][k] = make_float4(x[0], x[1], x[2], x[3]);
+            mk[j][k] = __builtin_nontemporal_load(rec + g);
+            lk[j][k] = __builtin_nontemporal_load(rec + 16 + g);
           }
       }
     }
-    float mp = -INFINITY, lp = 0.0f;
-    if (tg < G && tr < nr) {
-      const float* rec = rec_of(c0 + tr);
-      mp = __builtin_nontemporal_load(rec + tg);
-      lp = __builtin_nontemporal_load(rec + 16 + tg);
-    }
-    s_m[str][tr][tg] = mp;
-    s_l[str][tr][tg] = lp;
-    __syncthreads();
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int qd = t + 256 * j;
-      if ((NSTR == 1 || nr > 0) && j < nj && qd < nq) {
-        const int g = qd / Q;
+      if (nr > 0 && j < nj && qd < nq) {
         float cm = mrun[j];
-        for (int k = 0; k < nr; ++k) cm = fmaxf(cm, s_m[str][k][g]);
+#pragma unroll
+        for (int k = 0; k < kRC; ++k)
+          if (k < nr) cm = fmaxf(cm, mk[j][k]);
         const float alpha = mrun[j] == -INFINITY ? 0.0f : fast_exp2(mrun[j] - cm);
         float4 s = make_float4(acc[j].x * alpha, acc[j].y * alpha, acc[j].z * alpha, acc[j].w * alpha);
         float ls = lrun[j] * alpha;
 #pragma unroll
         for (int k = 0; k < kRC; ++k)
           if (k < nr) {
-            const float mk = s_m[str][k][g];
-            const float wk = mk == -INFINITY ? 0.0f : fast_exp2(mk - cm);
+            const float wk = mk[j][k] == -INFINITY ? 0.0f : fast_exp2(mk[j][k] - cm);
             s.x = fmaf(wk, v[j][k].x, s.x);
             s.y = fmaf(wk, v[j][k].y, s.y);
             s.z = fmaf(wk, v[j][k].z, s.z);
             s.w = fmaf(wk, v[j][k].w, s.w);
-            ls = fmaf(wk, s_l[str][k][g], ls);
+            ls = fmaf(wk, lk[j][k], ls);
           }
         acc[j] = s;
         lrun[j] = ls;
         mrun[j] = cm;
       }
     }
-    __syncthreads();  // the next chunk overwrites s_m / s_l
-  }
+  };
+  round(0);
+  for (int rd = 1; rd < rounds; ++rd) round(rd);
   if constexpr (NSTR > 1) {
     // Streams 1.. hand their state to stream 0, which folds them in stream order with weights
     // exp2(m_s - M), M the largest m_s (an empty stream, m = -inf, weighs 0).
