@@ -45,6 +45,8 @@ HIPCC_FLAGS = [
 # not preload.
 FILE_FLAGS = {
     "paged_decode_stream.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=3"],
+    # The read probe (the ceiling the decode kernel is compared with) launches the same way.
+    "hbm_probe.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=3"],
 }
 
 
