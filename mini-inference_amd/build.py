@@ -47,6 +47,8 @@ FILE_FLAGS = {
     "paged_decode_stream.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=3"],
     # The read probe (the ceiling the decode kernel is compared with) launches the same way.
     "hbm_probe.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=3"],
+    # The KV append takes its slot list and source rows as leading arguments in the same way.
+    "kv_append.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=3"],
 }
 
 

@@ -30,8 +30,28 @@ struct AppendArgs {
   int log2_bs;
 };
 
+// An empty asm that takes a loaded chunk and its slot as operands: both loads are issued
+// before it and waited for together.
+__device__ __forceinline__ void pin(uint4& v, int64_t& s) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w), "+v"(s));
+}
+__device__ __forceinline__ void pin(uint2& v, int64_t& s) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(s)); }
+__device__ __forceinline__ void pin(uint32_t& v, int64_t& s) { asm volatile("" : "+v"(v), "+v"(s)); }
+__device__ __forceinline__ void pin(uint16_t& v, int64_t& s) {
+  uint32_t w = v;
+  asm volatile("" : "+v"(w), "+v"(s));
+  v = static_cast<uint16_t>(w);
+}
+
+// The slot list and the source rows come as leading arguments, preloaded into scalar
+// registers at wave launch (the build's kernel-argument preloading for this file), and each
+// lane reads its source chunk before its slot is tested: the source does not depend on the
+// slot, so the slot and the row arrive in the same memory round trip and only the store waits
+// for both.
 template <int CHUNK>
-__global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
+__global__ __launch_bounds__(256) void kv_append_kernel(const int64_t* __restrict__ slots,
+                                                        const char* __restrict__ k_src,
+                                                        const char* __restrict__ v_src, AppendArgs a) {
   using V = typename ChunkT<CHUNK>::T;
   const uint32_t cpr = static_cast<uint32_t>(a.row_bytes / CHUNK);  // chunks per (token, head) row
   const uint32_t per_side = static_cast<uint32_t>(a.n_tokens) * a.hkv * cpr;
@@ -43,15 +63,20 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
     const uint32_t th = j / cpr;
     const uint32_t h = th % static_cast<uint32_t>(a.hkv);
     const int64_t tok = th / static_cast<uint32_t>(a.hkv);
-    const int64_t slot = a.slots[tok];
+    const char* src = (is_v ? v_src + tok * a.v_st + h * a.v_sh : k_src + tok * a.k_st + h * a.k_sh) +
+                      static_cast<int64_t>(c) * CHUNK;
+    V val = *reinterpret_cast<const V*>(src);
+    int64_t slot = slots[tok];
+    // Both values pass through an empty asm before the slot is tested: the compiler issues
+    // both loads and waits once, instead of sinking the source load into the store's branch
+    // (its only use) and reading it one round trip after the slot.
+    pin(val, slot);
     if (slot < 0 || slot >= a.n_slots) continue;  // padding row or invalid slot: no write
     const int64_t blk = slot >> a.log2_bs;
     const int64_t off = slot & (a.block_size - 1);
     const int64_t dst_row = (blk * a.hkv + h) * a.block_size + off;
-    const char* src = (is_v ? a.v_src + tok * a.v_st + h * a.v_sh : a.k_src + tok * a.k_st + h * a.k_sh) +
-                      static_cast<int64_t>(c) * CHUNK;
     char* dst = (is_v ? a.v_cache : a.k_cache) + dst_row * a.row_bytes + static_cast<int64_t>(c) * CHUNK;
-    *reinterpret_cast<V*>(dst) = *reinterpret_cast<const V*>(src);
+    *reinterpret_cast<V*>(dst) = val;
   }
 }
 
@@ -105,10 +130,10 @@ extern "C" int mip_kv_append(const void* k_src, const void* v_src, int64_t k_str
   const int blocks = static_cast<int>(blocks64 < 65536 ? blocks64 : 65536);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (chunk) {
-    case 16: hipLaunchKernelGGL(kv_append_kernel<16>, dim3(blocks), dim3(threads), 0, s, a); break;
-    case 8:  hipLaunchKernelGGL(kv_append_kernel<8>, dim3(blocks), dim3(threads), 0, s, a); break;
-    case 4:  hipLaunchKernelGGL(kv_append_kernel<4>, dim3(blocks), dim3(threads), 0, s, a); break;
-    default: hipLaunchKernelGGL(kv_append_kernel<2>, dim3(blocks), dim3(threads), 0, s, a); break;
+    case 16: hipLaunchKernelGGL(kv_append_kernel<16>, dim3(blocks), dim3(threads), 0, s, a.slots, a.k_src, a.v_src, a); break;
+    case 8:  hipLaunchKernelGGL(kv_append_kernel<8>, dim3(blocks), dim3(threads), 0, s, a.slots, a.k_src, a.v_src, a); break;
+    case 4:  hipLaunchKernelGGL(kv_append_kernel<4>, dim3(blocks), dim3(threads), 0, s, a.slots, a.k_src, a.v_src, a); break;
+    default: hipLaunchKernelGGL(kv_append_kernel<2>, dim3(blocks), dim3(threads), 0, s, a.slots, a.k_src, a.v_src, a); break;
   }
   return status_from_hip(hipGetLastError());
 }
