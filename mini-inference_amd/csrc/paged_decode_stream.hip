@@ -889,7 +889,7 @@ constexpr int kStreamParts = 16;
 // has 128 registers, and the chunk buffer alone takes 128). With runs > 1 (at most 16
 // segments), a segment of more than NSTR chunks is cut into runs of consecutive pieces, one
 // workgroup each, whose states paged_decode_stream_fold combines.
-template <int DT, int D, bool FUSED, bool PLANNED, int NSTR>
+template <int DT, int D, bool FUSED, bool PLANNED, int NSTR, int NJ>
 __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const int32_t* __restrict__ plan,
                                                                        int32_t plan_seg_off, int32_t hkv,
                                                                        StreamArgs sa) {
@@ -1020,8 +1020,10 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
   auto rec_of = [&](int r) -> const float* {
     return sa.ws_rec + (static_cast<int64_t>(gw_lo + r) * 2 + (r == 0 && lo_split ? 1 : 0)) * REC;
   };
-  // Passes over chunks of 16 records with an online maximum per row. Every thread owns up
-  // to two quads of four output columns of one row; the quads' partial sums of a chunk are
+  // Passes over chunks of 16 records with an online maximum per row. Every thread owns NJ
+  // quads of four output columns of one row (NJ = 2 only where a segment has more than 256
+  // quads, 9 to 16 heads at head_dim 128: the registers of a second quad would halve the
+  // merge's occupancy everywhere else); the quads' partial sums of a chunk are
   // loaded together with the row's (m, l) pairs, so a chunk costs one memory round trip.
   // Stream str takes chunks str, str + NSTR, ... (a round count uniform over the workgroup,
   // so every thread reaches the barrier of the stream fold below).
@@ -1030,31 +1032,29 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
   const int str = NSTR > 1 ? static_cast<int>(threadIdx.x) / 256 : 0;
   const int t = NSTR > 1 ? static_cast<int>(threadIdx.x) % 256 : static_cast<int>(threadIdx.x);
   const int nq = G * Q;  // quads per (kv head, sequence): at most 512
-  const int nj = nq > 256 ? 2 : 1;
-  float4 acc[2];
-  float mrun[2], lrun[2];
+  float4 acc[NJ];
+  float mrun[NJ], lrun[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     mrun[j] = -INFINITY;
     lrun[j] = 0.0f;
   }
   const int rounds = ((np + kRC - 1) / kRC + NSTR - 1) / NSTR;
-  // One round as a function, called for the first round outside the loop over the others: in
-  // a loop the compiler waits before each load for the same registers' load of the previous
-  // round, which serialises a chunk's loads into one round trip per record.
+  // One round as a function, called for the first round outside the loop over the others, so
+  // that the common single-round call has no loop-carried state at all.
   auto round = [&](int rd) __attribute__((always_inline)) {
     const int c0 = p0 + (rd * NSTR + str) * kRC;  // first piece of this stream's chunk
     const int nr = c0 >= p0 + np ? 0 : (p0 + np - c0 < kRC ? p0 + np - c0 : kRC);  // 0: no chunk this round
     // Each thread loads its own row's (m, l) pair of every record of the chunk beside the
     // record's partial sums, so the chunk is folded in registers right after its one round
     // trip (no exchange through LDS, no barrier). Records are read once: nontemporal loads.
-    float4 v[2][kRC];
-    float mk[2][kRC], lk[2][kRC];
+    float4 v[NJ][kRC];
+    float mk[NJ][kRC], lk[NJ][kRC];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int qd = t + 256 * j;
-      if (j < nj && qd < nq) {
+      if (qd < nq) {
         const int g = qd / Q, col = (qd % Q) * 4;
 #pragma unroll
         for (int k = 0; k < kRC; ++k)
@@ -1068,9 +1068,9 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
       }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int qd = t + 256 * j;
-      if (nr > 0 && j < nj && qd < nq) {
+      if (nr > 0 && qd < nq) {
         float cm = mrun[j];
 #pragma unroll
         for (int k = 0; k < kRC; ++k)
@@ -1093,17 +1093,21 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
         mrun[j] = cm;
       }
     }
+    // Every load of this round has been folded; saying so lets the next round issue its
+    // loads back to back (without it the compiler waits before each one for the same
+    // registers' load of the previous round).
+    wait_vmcnt<0>();
   };
   round(0);
   for (int rd = 1; rd < rounds; ++rd) round(rd);
   if constexpr (NSTR > 1) {
     // Streams 1.. hand their state to stream 0, which folds them in stream order with weights
     // exp2(m_s - M), M the largest m_s (an empty stream, m = -inf, weighs 0).
-    __shared__ float4 s_acc[NSTR - 1][2][256];
-    __shared__ float2 s_ml[NSTR - 1][2][256];
+    __shared__ float4 s_acc[NSTR - 1][NJ][256];
+    __shared__ float2 s_ml[NSTR - 1][NJ][256];
     if (str > 0) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         s_acc[str - 1][j][t] = acc[j];
         s_ml[str - 1][j][t] = make_float2(mrun[j], lrun[j]);
       }
@@ -1111,7 +1115,7 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
     __syncthreads();
     if (str > 0) return;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       float mm = mrun[j];
 #pragma unroll
       for (int u = 0; u < NSTR - 1; ++u) mm = fmaxf(mm, s_ml[u][j][t].x);
@@ -1138,9 +1142,9 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
     // Second-level record of run z: m[16] | l[16] | acc[G][D], as the stream kernel's records.
     float* rec = sa.ws_part + ((static_cast<int64_t>(b) * a.hkv + kvh) * Z + z) * REC;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int qd = t + 256 * j;
-      if (j < nj && qd < nq) {
+      if (qd < nq) {
         const int g = qd / Q, col = (qd % Q) * 4;
         *reinterpret_cast<float4*>(rec + 32 + g * D + col) = acc[j];
         if (col == 0) {
@@ -1153,9 +1157,9 @@ __global__ __launch_bounds__(256 * NSTR) void paged_decode_stream_merge(const in
     return;
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int qd = t + 256 * j;
-    if (j < nj && qd < nq) {
+    if (qd < nq) {
       const int g = qd / Q, col = (qd % Q) * 4;
       const float inv = lrun[j] > 0.0f ? 1.0f / lrun[j] : 0.0f;
       S* o = out_base + static_cast<int64_t>(b) * a.out_sb + static_cast<int64_t>(kvh * G + g) * a.out_sh + col;
@@ -1376,19 +1380,20 @@ struct StreamPick {
 template <int DT, int D, int QR>
 StreamPick pick_one() {
   constexpr int NS = D == 64 ? MIP_STREAM_STAGES_D64 : MIP_STREAM_STAGES_D128;
+  constexpr int NJ = QR * D / 4 > 256 ? 2 : 1;  // merge quads per thread: at most QR heads of D / 4 quads
   StreamPick p;
   p.main[0][0] = paged_decode_stream<DT, D, QR, NS, false>;
   p.main[0][1] = paged_decode_stream_tiles<DT, D, QR, NS, false>;
   p.main[1][0] = paged_decode_stream<DT, D, QR, NS, true>;
   p.main[1][1] = paged_decode_stream_tiles<DT, D, QR, NS, true>;
-  p.merge[0][0][0] = paged_decode_stream_merge<DT, D, false, false, 1>;
-  p.merge[0][1][0] = paged_decode_stream_merge<DT, D, false, true, 1>;
-  p.merge[1][0][0] = paged_decode_stream_merge<DT, D, true, false, 1>;
-  p.merge[1][1][0] = paged_decode_stream_merge<DT, D, true, true, 1>;
-  p.merge[0][0][1] = paged_decode_stream_merge<DT, D, false, false, kWideMergeStreams>;
-  p.merge[0][1][1] = paged_decode_stream_merge<DT, D, false, true, kWideMergeStreams>;
-  p.merge[1][0][1] = paged_decode_stream_merge<DT, D, true, false, kWideMergeStreams>;
-  p.merge[1][1][1] = paged_decode_stream_merge<DT, D, true, true, kWideMergeStreams>;
+  p.merge[0][0][0] = paged_decode_stream_merge<DT, D, false, false, 1, NJ>;
+  p.merge[0][1][0] = paged_decode_stream_merge<DT, D, false, true, 1, NJ>;
+  p.merge[1][0][0] = paged_decode_stream_merge<DT, D, true, false, 1, NJ>;
+  p.merge[1][1][0] = paged_decode_stream_merge<DT, D, true, true, 1, NJ>;
+  p.merge[0][0][1] = paged_decode_stream_merge<DT, D, false, false, kWideMergeStreams, NJ>;
+  p.merge[0][1][1] = paged_decode_stream_merge<DT, D, false, true, kWideMergeStreams, NJ>;
+  p.merge[1][0][1] = paged_decode_stream_merge<DT, D, true, false, kWideMergeStreams, NJ>;
+  p.merge[1][1][1] = paged_decode_stream_merge<DT, D, true, true, kWideMergeStreams, NJ>;
   p.fold[0] = paged_decode_stream_fold<DT, D, false>;
   p.fold[1] = paged_decode_stream_fold<DT, D, true>;
   p.ring_bytes = NS * Ring<D, QR>::STAGE;
