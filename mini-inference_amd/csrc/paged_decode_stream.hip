@@ -885,8 +885,8 @@ constexpr int kStreamParts = 16;
 // stream with its own online maximum), and stream 0 then combines the streams' states in
 // stream order. NSTR = 1 serves batches of many segments (each segment has few pieces);
 // NSTR = 2 serves a few long sequences, whose segments have up to a few hundred pieces (two
-// streams keep a chunk's 16 partial sums per thread in registers: at 1024 threads a thread
-// has 128 registers, and the chunk buffer alone takes 128). With runs > 1 (at most 16
+// streams, not more: each thread keeps a chunk's 16 partial sums and (m, l) pairs per quad in
+// registers, and at 1024 threads a thread has 128 registers). With runs > 1 (at most 16
 // segments), a segment of more than NSTR chunks is cut into runs of consecutive pieces, one
 // workgroup each, whose states paged_decode_stream_fold combines.
 template <int DT, int D, bool FUSED, bool PLANNED, int NSTR, int NJ>
@@ -1364,10 +1364,12 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(PlanArg
   }
 }
 
-// Every stream kernel takes the plan pointer and two of its word offsets ahead of the argument
-// block: the build preloads these leading scalar arguments into scalar registers (gfx950
-// kernel-argument preloading), so a planned kernel issues its first plan reads without first
-// waiting for a load of its arguments. Kernels that do not use them ignore them.
+// Every stream kernel takes the plan pointer and two scalars ahead of the argument block (the
+// main kernel: the plan's descriptor offset and slots per wavefront; the merge: the plan's
+// segment-record offset and the kv-head count). The build preloads these leading arguments
+// into scalar registers (gfx950 kernel-argument preloading), so a planned kernel issues its
+// first plan reads without first waiting for a load of its arguments. Kernels that do not use
+// them ignore them.
 using StreamFn = void (*)(const int32_t*, int32_t, int32_t, StreamArgs);
 
 struct StreamPick {
