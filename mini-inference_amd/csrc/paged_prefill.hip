@@ -115,23 +115,23 @@ struct PShape {
   static_assert(NLD >= 1 && NLD * kPW * kWave == kKT * CPR, "tile must split evenly over the workgroup");
 };
 
-// One work item: new tokens [blk * TQ, blk * TQ + TQ) of sequence s against kv head kvh.
-// smem holds the two K | V stages, s_ok[stage][key] whether a key row is a real key (valid
-// block id), byte w of s_wok[stage] whether every key row wavefront w loaded is. Called by
-// the whole workgroup (the barriers inside are workgroup-wide).
+// One work item: new tokens [tok_lo, tok_end) of sequence s against kv head kvh, at most
+// TQ = 64 NC / G of them (the rows of NC column blocks per wavefront). smem holds the two
+// K | V stages, s_ok[stage][key] whether a key row is a real key (valid block id), byte w of
+// s_wok[stage] whether every key row wavefront w loaded is. Called by the whole workgroup
+// (the barriers inside are workgroup-wide).
 template <int DT, int D, int NC>
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int s, int blk, char* smem,
-                                             uint8_t (*s_ok)[kKT], uint32_t* s_wok) {
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int s, int tok_lo, int tok_end,
+                                             char* smem, uint8_t (*s_ok)[kKT], uint32_t* s_wok) {
   using P = PShape<D>;
   using Ops = MfmaOps<DT>;
   constexpr int RB = P::RB, CPR = P::CPR, KC = P::KC, MT = P::MT;
-  const int TQ = a.tq;  // tokens per workgroup
+  const int TQ = kPW * NC * 16 / a.group;  // token capacity of the item's rows
 
   const int q0 = a.cu_q[s];
   const int n_s = a.cu_q[s + 1] - q0;
-  const int tok_lo = blk * TQ;
   if (tok_lo >= n_s) return;
-  const int tok_hi = tok_lo + TQ < n_s ? tok_lo + TQ : n_s;
+  const int tok_hi = tok_end < n_s ? tok_end : n_s;
   const int start = a.ctx_start[s] > 0 ? a.ctx_start[s] : 0;
   const int cap = a.max_blocks * a.bs;
   int p_last = start + tok_hi - 1;
@@ -439,7 +439,8 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
   static_assert(kPW == 4, "one byte per wavefront in s_wok");
   if constexpr (!PERSIST) {
     // One workgroup per (kv head, sequence, block), blocks of a sequence latest first.
-    prefill_item<DT, D, NC>(a, blockIdx.x, blockIdx.y, gridDim.z - 1 - blockIdx.z, smem, s_ok, s_wok);
+    const int blk = gridDim.z - 1 - blockIdx.z;
+    prefill_item<DT, D, NC>(a, blockIdx.x, blockIdx.y, blk * TQ, blk * TQ + TQ, smem, s_ok, s_wok);
   } else {
     __shared__ int s_nb[kMaxSeqs];          // blocks of sequence s
     __shared__ int s_seq[kMaxSeqs];         // sequences by blocks, descending
@@ -480,23 +481,52 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
     if (tid == 0) s_ipre[0] = 0;
     __syncthreads();
     const int total = s_ipre[zb];
-    // Rounds of gridDim.x items, alternating direction, so a workgroup that drew a long item in
-    // one round draws a short one in the next.
-    const int G = gridDim.x;
-    for (int r = 0; r * G < total; ++r) {
-      const int it = r * G + ((r & 1) ? G - 1 - static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x));
-      if (it >= total) continue;
+    // Item it of the list: (sequence, kv head, block of TQ tokens).
+    auto item = [&](int it, int& seq, int& kvh, int& blk) __attribute__((always_inline)) {
       int lo = 0, hi = zb - 1;  // the level k with s_ipre[k] <= it < s_ipre[k + 1]
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
         if (s_ipre[mid] <= it) lo = mid; else hi = mid - 1;
       }
       const int rem = it - s_ipre[lo];
-      const int seq = __builtin_amdgcn_readfirstlane(s_seq[rem / a.hkv]);
-      const int kvh = __builtin_amdgcn_readfirstlane(rem % a.hkv);
-      const int blk = __builtin_amdgcn_readfirstlane(zb - 1 - lo);
-      prefill_item<DT, D, NC>(a, kvh, seq, blk, smem, s_ok, s_wok);
+      seq = __builtin_amdgcn_readfirstlane(s_seq[rem / a.hkv]);
+      kvh = __builtin_amdgcn_readfirstlane(rem % a.hkv);
+      blk = __builtin_amdgcn_readfirstlane(zb - 1 - lo);
+    };
+    // Whole rounds of gridDim.x items, alternating direction, so a workgroup that drew a long
+    // item in one round draws a short one in the next.
+    const int G = gridDim.x, wg = static_cast<int>(blockIdx.x);
+    const int full = total / G, last = total - full * G;
+    for (int r = 0; r < full; ++r) {
+      int seq, kvh, blk;
+      item(r * G + ((r & 1) ? G - 1 - wg : wg), seq, kvh, blk);
+      prefill_item<DT, D, NC>(a, kvh, seq, blk * TQ, blk * TQ + TQ, smem, s_ok, s_wok);
     }
+    if (last == 0) return;
+    // The last, partial round holds the shortest items (or, in a call of fewer items than
+    // workgroups, all of them) and leaves G - last workgroups idle. Up to that many of its
+    // items (the longest first) are cut into two halves of half the column blocks per
+    // wavefront, one workgroup each, so the round ends after about half an item where it
+    // can. Rows do not depend on one another: halves need no merge. A half does a little
+    // more than half the work of its item (every key tile is still staged and walked), so
+    // only the idle workgroups take halves; quarters were slower for that reason.
+    const int u = (full & 1) ? G - 1 - wg : wg;  // this workgroup's place in the round
+    constexpr int NC2 = NC / 2;
+    const int tq2 = NC2 > 0 ? kPW * NC2 * 16 / a.group : 0;
+    const int n_split = NC2 > 0 && 2 * tq2 >= TQ ? (last < G - last ? last : G - last) : 0;
+    if (u >= last + n_split) return;
+    int seq, kvh, blk;
+    if (u < 2 * n_split) {
+      if constexpr (NC2 > 0) {
+        item(full * G + u / 2, seq, kvh, blk);
+        const int t0 = blk * TQ + (u & 1) * tq2, t_end = blk * TQ + TQ;
+        prefill_item<DT, D, (NC2 > 0 ? NC2 : 1)>(a, kvh, seq, t0, t0 + tq2 < t_end ? t0 + tq2 : t_end, smem, s_ok,
+                                                   s_wok);
+      }
+      return;
+    }
+    item(full * G + u - n_split, seq, kvh, blk);
+    prefill_item<DT, D, NC>(a, kvh, seq, blk * TQ, blk * TQ + TQ, smem, s_ok, s_wok);
   }
 }
 
@@ -528,8 +558,11 @@ int launch_shape(PrefillArgs a, int num_seqs, int max_q_len, hipStream_t s) {
   // since the workgroups past a sequence's end occupy the dispatcher.
   static const int grid_cap = persistent_grid<DT, D, NC>();
   const int64_t items = static_cast<int64_t>(a.hkv) * num_seqs * zb;
+  // A call of fewer items than the device holds workgroups cuts them into halves, so the grid
+  // may hold twice as many workgroups.
+  const int64_t units = items * 2;
   if (grid_cap > 0 && num_seqs <= kMaxSeqs && zb <= kMaxLevels) {
-    const int grid = static_cast<int>(items < grid_cap ? items : grid_cap);
+    const int grid = static_cast<int>(units < grid_cap ? units : grid_cap);
     hipLaunchKernelGGL((paged_prefill_kernel<DT, D, NC, true>), dim3(grid), dim3(kPW * kWave), 0, s, a);
   } else {
     if (num_seqs > 65535 || zb > 65535) return MIP_EUNSUPPORTED;

@@ -290,3 +290,30 @@ def test_paged_prefill_grid_fallbacks(gpu):
         want = ref.prefill_attention_f64(qc[rows], kp, vp, [table], [start + r0], [32], bs)
         err = float((np.abs(oc[rows] - want) - half_ulp(want, dtype)).max())
         assert err <= 2e-3, (r0, err)
+
+
+# Work lists whose last, partial round of the persistent grid takes each form on a device of
+# 512 resident workgroups (256 CUs, two each): (starts, lengths, hq, hkv, d, bs).
+LAST_ROUND_CASES = [
+    ([0] * 58, [252] * 58, 14, 2, 64, 16),    # 812 items: one whole round, then 212 items halved + 88 whole
+    ([100] * 64, [288] * 64, 14, 2, 64, 16),  # 1024 items: two whole rounds, nothing left over
+    ([7] * 30, [36] * 30, 14, 2, 64, 16),     # 60 items, all halved (grid of 120)
+    ([0] * 21, [200] * 21, 10, 2, 64, 16),    # group 5: 51 tokens per item do not fit two halves of 25
+    ([40] * 9, [130] * 9, 28, 4, 128, 32),    # head_dim 128: items of 18 tokens in halves of 9
+]
+
+
+@pytest.mark.parametrize("case", range(len(LAST_ROUND_CASES)))
+def test_paged_prefill_last_round_pieces(gpu, case):
+    """The persistent kernel cuts items of its last, partial round into two halves of half the
+    rows where workgroups would otherwise idle; every row of every sequence is checked against
+    float64, whichever way its item ran."""
+    from engine import paged_ops
+
+    starts, lengths, hq, hkv, d, bs = LAST_ROUND_CASES[case]
+    announce(f"paged_prefill last-round pieces: {len(lengths)} x {lengths[0]} after {starts[0]}, hq={hq} hkv={hkv} d={d}")
+    dev, want = build(gpu, "float16", d, hq, hkv, bs, starts, lengths, seed=40 + case)
+    out = paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], max(lengths))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert float((np.abs(got - want) - half_ulp(want, "float16")).max()) <= 2e-3
