@@ -413,18 +413,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
 // index, highest first (later tokens see more keys), then by sorted sequence, then kv head,
 // so the longest items start first. Limits: kMaxSeqs sequences, kMaxLevels blocks each.
 constexpr int kMaxSeqs = 1024;
-constexpr int kMaxLevels = kPW * kWave - 1;  // 255: one scan entry per thread
-
-__device__ __forceinline__ int block_inclusive_scan(int x, int* s_wtot) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  const int incl = decode::wave_inclusive_scan(x, lane);
-  if (lane == kWave - 1) s_wtot[w] = incl;
-  __syncthreads();
-  int off = 0;
-  for (int j = 0; j < w; ++j) off += s_wtot[j];
-  __syncthreads();  // s_wtot is reused by the next scan
-  return incl + off;
-}
+constexpr int kMaxLevels = 255;
 
 // Two wavefronts per SIMD is the occupancy the register file allows at these tile sizes;
 // saying so lets the compiler use up to 256 registers instead of spilling.
@@ -444,41 +433,52 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
   } else {
     __shared__ int s_nb[kMaxSeqs];          // blocks of sequence s
     __shared__ int s_seq[kMaxSeqs];         // sequences by blocks, descending
-    __shared__ int s_cnt[kMaxLevels + 1];   // histogram, then sequences with more than v blocks
+    __shared__ int s_cnt[kMaxLevels + 1];   // histogram: sequences with v blocks
+    __shared__ int s_gt[kMaxLevels + 1];    // sequences with more than v blocks
     __shared__ int s_fill[kMaxLevels + 1];
     __shared__ int s_ipre[kMaxLevels + 1];  // first item of the k-th level, highest level first
-    __shared__ int s_wtot[kPW];
-    const int tid = threadIdx.x, S = a.num_seqs, zb = a.zb;
-    for (int v = tid; v <= zb; v += kPW * kWave) {
-      s_cnt[v] = 0;
-      s_fill[v] = 0;
+    const int S = a.num_seqs, zb = a.zb;
+    // One wavefront builds the list with wavefront scans (no workgroup barrier until it is
+    // done); LDS operations of one wavefront take effect in program order.
+    if (threadIdx.x < kWave) {
+      const int lane = threadIdx.x;
+      for (int v = lane; v <= zb; v += kWave) {
+        s_cnt[v] = 0;
+        s_fill[v] = 0;
+      }
+      for (int q = lane; q < S; q += kWave) {
+        const int n = a.cu_q[q + 1] - a.cu_q[q];
+        int nb = n > 0 ? (n + TQ - 1) / TQ : 0;
+        nb = nb < zb ? nb : zb;
+        s_nb[q] = nb;
+        atomicAdd(&s_cnt[nb], 1);
+      }
+      // s_gt[v] = sum of s_cnt[u] over u > v, bins taken from the top (s_gt[zb] = 0).
+      int carry = 0;
+      for (int base = 0; base <= zb; base += kWave) {
+        const int v = zb - base - lane;
+        const int c = v >= 0 && v < zb ? s_cnt[v + 1] : 0;
+        const int incl = decode::wave_inclusive_scan(c, lane) + carry;
+        if (v >= 0) s_gt[v] = incl;
+        carry = __shfl(incl, kWave - 1);
+      }
+      // Sequences with nb blocks take places s_gt[nb] onwards (descending by blocks).
+      for (int q = lane; q < S; q += kWave) {
+        const int nb = s_nb[q];
+        s_seq[s_gt[nb] + atomicAdd(&s_fill[nb], 1)] = q;
+      }
+      // Items of level lv = zb - 1 - k (k-th from the top): one per (sequence with more than
+      // lv blocks, kv head).
+      carry = 0;
+      for (int base = 0; base < zb; base += kWave) {
+        const int k = base + lane;
+        const int items = k < zb ? s_gt[zb - 1 - k] * a.hkv : 0;
+        const int incl = decode::wave_inclusive_scan(items, lane) + carry;
+        if (k < zb) s_ipre[k + 1] = incl;
+        carry = __shfl(incl, kWave - 1);
+      }
+      if (lane == 0) s_ipre[0] = 0;
     }
-    __syncthreads();
-    for (int q = tid; q < S; q += kPW * kWave) {
-      const int n = a.cu_q[q + 1] - a.cu_q[q];
-      int nb = n > 0 ? (n + TQ - 1) / TQ : 0;
-      nb = nb < zb ? nb : zb;
-      s_nb[q] = nb;
-      atomicAdd(&s_cnt[nb], 1);
-    }
-    __syncthreads();
-    // Thread t takes bin zb - t: the inclusive scan counts the sequences with at least that many
-    // blocks, i.e. more than zb - t - 1.
-    const int hv = tid <= zb ? s_cnt[zb - tid] : 0;
-    const int ge = block_inclusive_scan(hv, s_wtot);
-    if (tid < zb) s_cnt[zb - tid - 1] = ge;  // sequences with more than zb - tid - 1 blocks
-    if (tid == 0) s_cnt[zb] = 0;
-    __syncthreads();
-    for (int q = tid; q < S; q += kPW * kWave) {
-      const int nb = s_nb[q];
-      s_seq[s_cnt[nb] + atomicAdd(&s_fill[nb], 1)] = q;
-    }
-    // Items of level lv = zb - 1 - k (k-th from the top): one per (sequence with more than lv
-    // blocks, kv head).
-    const int items = tid < zb ? s_cnt[zb - 1 - tid] * a.hkv : 0;
-    const int incl = block_inclusive_scan(items, s_wtot);
-    if (tid < zb) s_ipre[tid + 1] = incl;
-    if (tid == 0) s_ipre[0] = 0;
     __syncthreads();
     const int total = s_ipre[zb];
     // Item it of the list: (sequence, kv head, block of TQ tokens).
