@@ -268,8 +268,9 @@ def test_paged_prefill_grid_fallbacks(gpu):
     got = out.float().cpu().numpy()
     assert float((np.abs(got - want) - half_ulp(want, "float16")).max()) <= 2e-3
 
-    announce("paged_prefill one sequence of 8200 new tokens after 100 cached (per-item grid)")
-    dtype, d, hq, hkv, bs, start, n = "bfloat16", 64, 14, 2, 16, 100, 8200
+    # 9,300 tokens at 36 per work item (14q/2kv) are 259 blocks: past the persistent list's 255.
+    announce("paged_prefill one sequence of 9300 new tokens after 100 cached (per-item grid)")
+    dtype, d, hq, hkv, bs, start, n = "bfloat16", 64, 14, 2, 16, 100, 9300
     nblk = (start + n + bs - 1) // bs
     ids = list(range(nblk + 4))
     rnd.shuffle(ids)
@@ -285,7 +286,7 @@ def test_paged_prefill_grid_fallbacks(gpu):
     torch.cuda.synchronize()
     kp, vp = k_pool.float().cpu().numpy(), v_pool.float().cpu().numpy()
     qc, oc = q.float().cpu().numpy(), out.float().cpu().numpy()
-    for r0 in (0, 31, 4000, 8100, n - 33):
+    for r0 in (0, 31, 4000, 9100, n - 33):
         rows = slice(r0, r0 + 32)
         want = ref.prefill_attention_f64(qc[rows], kp, vp, [table], [start + r0], [32], bs)
         err = float((np.abs(oc[rows] - want) - half_ulp(want, dtype)).max())
