@@ -120,19 +120,19 @@ struct PShape {
 // K | V stages, s_ok[stage][key] whether a key row is a real key (valid block id), byte w of
 // s_wok[stage] whether every key row wavefront w loaded is. Called by the whole workgroup
 // (the barriers inside are workgroup-wide).
+// q0, n_s and start are cu_q[s], cu_q[s + 1] - cu_q[s] and ctx_start[s] (the caller reads them).
 template <int DT, int D, int NC>
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int s, int tok_lo, int tok_end,
-                                             char* smem, uint8_t (*s_ok)[kKT], uint32_t* s_wok) {
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int s, int q0, int n_s, int start_in,
+                                             int tok_lo, int tok_end, char* smem, uint8_t (*s_ok)[kKT],
+                                             uint32_t* s_wok) {
   using P = PShape<D>;
   using Ops = MfmaOps<DT>;
   constexpr int RB = P::RB, CPR = P::CPR, KC = P::KC, MT = P::MT;
   const int TQ = kPW * NC * 16 / a.group;  // token capacity of the item's rows
 
-  const int q0 = a.cu_q[s];
-  const int n_s = a.cu_q[s + 1] - q0;
   if (tok_lo >= n_s) return;
   const int tok_hi = tok_end < n_s ? tok_end : n_s;
-  const int start = a.ctx_start[s] > 0 ? a.ctx_start[s] : 0;
+  const int start = start_in > 0 ? start_in : 0;
   const int cap = a.max_blocks * a.bs;
   int p_last = start + tok_hi - 1;
   p_last = p_last < cap - 1 ? p_last : cap - 1;  // keys past the table are never read
@@ -428,9 +428,13 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
   static_assert(kPW == 4, "one byte per wavefront in s_wok");
   if constexpr (!PERSIST) {
     // One workgroup per (kv head, sequence, block), blocks of a sequence latest first.
-    const int blk = gridDim.z - 1 - blockIdx.z;
-    prefill_item<DT, D, NC>(a, blockIdx.x, blockIdx.y, blk * TQ, blk * TQ + TQ, smem, s_ok, s_wok);
+    const int blk = gridDim.z - 1 - blockIdx.z, s = blockIdx.y;
+    const int q0 = a.cu_q[s];
+    prefill_item<DT, D, NC>(a, blockIdx.x, s, q0, a.cu_q[s + 1] - q0, a.ctx_start[s], blk * TQ, blk * TQ + TQ, smem,
+                            s_ok, s_wok);
   } else {
+    __shared__ int s_cu[kMaxSeqs + 1];      // cu_q
+    __shared__ int s_st[kMaxSeqs];          // ctx_start
     __shared__ int s_nb[kMaxSeqs];          // blocks of sequence s
     __shared__ int s_seq[kMaxSeqs];         // sequences by blocks, descending
     __shared__ int s_cnt[kMaxLevels + 1];   // histogram: sequences with v blocks
@@ -447,7 +451,11 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
         s_fill[v] = 0;
       }
       for (int q = lane; q < S; q += kWave) {
-        const int n = a.cu_q[q + 1] - a.cu_q[q];
+        const int c0 = a.cu_q[q], c1 = a.cu_q[q + 1];
+        s_cu[q] = c0;
+        s_st[q] = a.ctx_start[q];
+        if (q == S - 1) s_cu[S] = c1;
+        const int n = c1 - c0;
         int nb = n > 0 ? (n + TQ - 1) / TQ : 0;
         nb = nb < zb ? nb : zb;
         s_nb[q] = nb;
@@ -500,7 +508,8 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
     for (int r = 0; r < full; ++r) {
       int seq, kvh, blk;
       item(r * G + ((r & 1) ? G - 1 - wg : wg), seq, kvh, blk);
-      prefill_item<DT, D, NC>(a, kvh, seq, blk * TQ, blk * TQ + TQ, smem, s_ok, s_wok);
+      prefill_item<DT, D, NC>(a, kvh, seq, s_cu[seq], s_cu[seq + 1] - s_cu[seq], s_st[seq], blk * TQ, blk * TQ + TQ,
+                              smem, s_ok, s_wok);
     }
     if (last == 0) return;
     // The last, partial round holds the shortest items (or, in a call of fewer items than
@@ -520,13 +529,14 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
       if constexpr (NC2 > 0) {
         item(full * G + u / 2, seq, kvh, blk);
         const int t0 = blk * TQ + (u & 1) * tq2, t_end = blk * TQ + TQ;
-        prefill_item<DT, D, (NC2 > 0 ? NC2 : 1)>(a, kvh, seq, t0, t0 + tq2 < t_end ? t0 + tq2 : t_end, smem, s_ok,
-                                                   s_wok);
+        prefill_item<DT, D, (NC2 > 0 ? NC2 : 1)>(a, kvh, seq, s_cu[seq], s_cu[seq + 1] - s_cu[seq], s_st[seq], t0,
+                                                   t0 + tq2 < t_end ? t0 + tq2 : t_end, smem, s_ok, s_wok);
       }
       return;
     }
     item(full * G + u - n_split, seq, kvh, blk);
-    prefill_item<DT, D, NC>(a, kvh, seq, blk * TQ, blk * TQ + TQ, smem, s_ok, s_wok);
+    prefill_item<DT, D, NC>(a, kvh, seq, s_cu[seq], s_cu[seq + 1] - s_cu[seq], s_st[seq], blk * TQ, blk * TQ + TQ, smem,
+                            s_ok, s_wok);
   }
 }
 
