@@ -237,7 +237,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
   f32x4_t acc[NC][MT];
   f32x4_t lacc[NC];  // row sums by MFMA against a ones block: every element holds row i16's sum
   float m[NC];
-  float mth[NC], nm[NC];  // m + kRescaleLog2 (the rescale threshold) and -m (0 while m = -inf)
+  float mth[NC], nm[NC];  // the rescale threshold (m + kRescaleLog2) / scale_log2, and -m (0 while m = -inf)
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     m[c] = -INFINITY;
@@ -327,26 +327,27 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
           for (int i = 0; i < 8; ++i) sv[c][i] = (kok[i] && kr[i] <= lim) ? sv[c][i] : -INFINITY;
         }
       }
-      // The rescale test on each lane's maximum, scaled once (the scale is positive).
+      // The rescale test on each lane's maximum of raw scores, against a threshold in raw
+      // units (the scale is positive).
       float mx[NC];
       bool need = false;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         mx[c] = fmax3(fmax3(sv[c][0], sv[c][1], sv[c][2]), fmax3(sv[c][3], sv[c][4], sv[c][5]),
-                      fmax2(sv[c][6], sv[c][7])) * a.scale_log2;
+                      fmax2(sv[c][6], sv[c][7]));
         need = need || mx[c] > mth[c];
       }
       if (__any(need)) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
           if (__any(mx[c] > mth[c])) {
-            const float mn = fmax2(m[c], max4(mx[c]));
+            const float mn = fmax2(m[c], max4(mx[c]) * a.scale_log2);
             const float alpha = (m[c] == -INFINITY) ? 0.0f : fast_exp2(m[c] - mn);
             lacc[c] *= alpha;
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[c][mt] *= alpha;
             m[c] = mn;
-            mth[c] = mn + kRescaleLog2;
+            mth[c] = (mn + kRescaleLog2) / a.scale_log2;
             // exp2(-inf - m) = 0 for any finite m; m stays -inf only while every score of the
             // row so far is -inf, and then exp2(-inf - 0) = 0 as well.
             nm[c] = mn == -INFINITY ? 0.0f : -mn;
