@@ -502,13 +502,17 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
       kvh = __builtin_amdgcn_readfirstlane(rem % a.hkv);
       blk = __builtin_amdgcn_readfirstlane(zb - 1 - lo);
     };
-    // Whole rounds of gridDim.x items, alternating direction, so a workgroup that drew a long
-    // item in one round draws a short one in the next.
-    const int G = gridDim.x, wg = static_cast<int>(blockIdx.x);
+    // Whole rounds of gridDim.x items. Workgroups b and b + G/2 share a CU (the grid is two
+    // workgroups per CU, dispatched one per CU first), and the older one, b, issues first and
+    // runs faster while both are busy. Even rounds go in list order; in odd rounds the first
+    // workgroups of the CUs take the longer half of the round in order, and the second ones
+    // the shorter half in reverse, so a second workgroup that drew a short item before draws
+    // the longest of its half.
+    const int G = gridDim.x, wg = static_cast<int>(blockIdx.x), H = G / 2;
     const int full = total / G, last = total - full * G;
     for (int r = 0; r < full; ++r) {
       int seq, kvh, blk;
-      item(r * G + ((r & 1) ? G - 1 - wg : wg), seq, kvh, blk);
+      item(r * G + ((r & 1) && wg >= H ? G - 1 - (wg - H) : wg), seq, kvh, blk);
       prefill_item<DT, D, NC>(a, kvh, seq, s_cu[seq], s_cu[seq + 1] - s_cu[seq], s_st[seq], blk * TQ, blk * TQ + TQ,
                               smem, s_ok, s_wok);
     }
