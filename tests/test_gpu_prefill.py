@@ -252,6 +252,35 @@ def test_prefill_context_matches_reference_formulation(gpu, prefix, dtype):
     assert [cache.lengths[s] for s in slots] == [a + b for a, b in zip(starts, new)]
 
 
+def _long_sequence_rows(gpu, rnd, start, n, seed, dtype="bfloat16"):
+    """One sequence of n new tokens after start cached ones (14q/2kv, d64, block 16); rows
+    sampled at the ends and in the middle against float64."""
+    from engine import paged_ops
+
+    d, hq, hkv, bs = 64, 14, 2, 16
+    nblk = (start + n + bs - 1) // bs
+    ids = list(range(nblk + 4))
+    rnd.shuffle(ids)
+    table = ids[:nblk]
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    tdt = getattr(torch, dtype)
+    k_pool = torch.randn(nblk + 5, hkv, bs, d, generator=g, device=gpu).to(tdt)
+    v_pool = torch.randn(nblk + 5, hkv, bs, d, generator=g, device=gpu).to(tdt)
+    qkv = torch.randn(n, (hq + 2 * hkv) * d, generator=g, device=gpu).to(tdt)
+    q = qkv[:, :hq * d].view(n, hq, d)
+    tab = torch.tensor([table], dtype=torch.int32, device=gpu)
+    cu = torch.tensor([0, n], dtype=torch.int32, device=gpu)
+    out = paged_ops.paged_prefill(q, k_pool, v_pool, tab, cu, torch.tensor([start], dtype=torch.int32, device=gpu), n)
+    torch.cuda.synchronize()
+    kp, vp = k_pool.float().cpu().numpy(), v_pool.float().cpu().numpy()
+    qc, oc = q.float().cpu().numpy(), out.float().cpu().numpy()
+    for r0 in (0, 31, n // 2, n - 200, n - 33):
+        rows = slice(r0, r0 + 32)
+        want = ref.prefill_attention_f64(qc[rows], kp, vp, [table], [start + r0], [32], bs)
+        err = float((np.abs(oc[rows] - want) - half_ulp(want, dtype)).max())
+        assert err <= 2e-3, (n, r0, err)
+
+
 def test_paged_prefill_grid_fallbacks(gpu):
     """The one-workgroup-per-item grid, taken past the persistent kernel's work-list limits:
     more than 1024 sequences, and one sequence with more than 255 blocks of new tokens (rows
@@ -270,27 +299,27 @@ def test_paged_prefill_grid_fallbacks(gpu):
 
     # 9,300 tokens at 36 per work item (14q/2kv) are 259 blocks: past the persistent list's 255.
     announce("paged_prefill one sequence of 9300 new tokens after 100 cached (per-item grid)")
-    dtype, d, hq, hkv, bs, start, n = "bfloat16", 64, 14, 2, 16, 100, 9300
-    nblk = (start + n + bs - 1) // bs
-    ids = list(range(nblk + 4))
-    rnd.shuffle(ids)
-    table = ids[:nblk]
-    g = torch.Generator(device=gpu).manual_seed(17)
-    k_pool = torch.randn(nblk + 5, hkv, bs, d, generator=g, device=gpu).to(torch.bfloat16)
-    v_pool = torch.randn(nblk + 5, hkv, bs, d, generator=g, device=gpu).to(torch.bfloat16)
-    qkv = torch.randn(n, (hq + 2 * hkv) * d, generator=g, device=gpu).to(torch.bfloat16)
-    q = qkv[:, :hq * d].view(n, hq, d)
-    tab = torch.tensor([table], dtype=torch.int32, device=gpu)
-    cu = torch.tensor([0, n], dtype=torch.int32, device=gpu)
-    out = paged_ops.paged_prefill(q, k_pool, v_pool, tab, cu, torch.tensor([start], dtype=torch.int32, device=gpu), n)
+    _long_sequence_rows(gpu, rnd, 100, 9300, seed=17)
+
+
+def test_paged_prefill_persistent_limits(gpu):
+    """The persistent kernel exactly at its work-list limits: 1024 sequences (the largest
+    index of the sequence arrays), and one sequence of 255 blocks of 36 new tokens (the top
+    level of the block histogram)."""
+    from engine import paged_ops
+
+    announce("paged_prefill 1024 short sequences (persistent grid, sequence limit)")
+    rnd = random.Random(29)
+    lengths = [rnd.randint(1, 3) for _ in range(1024)]
+    starts = [rnd.randint(0, 40) for _ in range(1024)]
+    dev, want = build(gpu, "float16", 64, 14, 2, 16, starts, lengths, seed=29)
+    out = paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], max(lengths))
     torch.cuda.synchronize()
-    kp, vp = k_pool.float().cpu().numpy(), v_pool.float().cpu().numpy()
-    qc, oc = q.float().cpu().numpy(), out.float().cpu().numpy()
-    for r0 in (0, 31, 4000, 9100, n - 33):
-        rows = slice(r0, r0 + 32)
-        want = ref.prefill_attention_f64(qc[rows], kp, vp, [table], [start + r0], [32], bs)
-        err = float((np.abs(oc[rows] - want) - half_ulp(want, dtype)).max())
-        assert err <= 2e-3, (r0, err)
+    got = out.float().cpu().numpy()
+    assert float((np.abs(got - want) - half_ulp(want, "float16")).max()) <= 2e-3
+
+    announce("paged_prefill one sequence of 9180 new tokens after 100 cached (persistent grid, 255 blocks)")
+    _long_sequence_rows(gpu, rnd, 100, 255 * 36, seed=31, dtype="float16")
 
 
 # Work lists whose last, partial round of the persistent grid takes each form on a device of
