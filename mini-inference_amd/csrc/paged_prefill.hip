@@ -21,7 +21,7 @@
 // one is computed); then each wavefront computes, for each 16-key half,
 //   S^T[16 keys x 16 rows] = K . Q^T      v_mfma_f32_16x16x32, D/32 steps (Q^T in registers)
 // and then, over all 32 keys,
-//   O^T[D x 16 rows]      += V^T . P^T    v_mfma_f32_16x16x32, D/16 tiles (bf16: P split hi + lo)
+//   O^T[D x 16 rows]      += V^T . P^T    v_mfma_f32_16x16x32, D/16 tiles (fp16 P; bf16 V staged as fp16)
 // with a base-2 online softmax per row, as in the decode kernels. Rows whose position is below
 // a key mask it out; a wavefront skips tiles that lie beyond all of its rows' positions, and a
 // column block skips the masking in steps whose keys all of its live rows see (most of them).
@@ -84,9 +84,27 @@ __device__ __forceinline__ float max4(float x) {
 }
 
 // P = exp2(s - m) lies in [0, 2^kRescaleLog2]. fp16 holds it to 2^-11 relative, enough for
-// the 2e-3 bound on outputs that are convex combinations of the values; bf16 (2^-8) is split
-// into a rounded part and its remainder, each multiplied by V^T.
-template <int DT> constexpr bool kSplitP = DT == MIP_BF16;
+// the 2e-3 bound on outputs that are convex combinations of the values; bf16 (2^-8) is not.
+// bf16 items therefore first run with V converted to fp16 as it is staged (bf16x8_to_f16x8:
+// exact for every value fp16 can hold), so P stays fp16 and the PV product is one fp16
+// MFMA; an item whose staged V holds a value fp16 cannot (|v| >= 65536, inf, NaN) runs again
+// with bf16 V and P split into a rounded part and its remainder, each multiplied by V^T.
+template <int DT, bool VF16> constexpr bool kSplitP = DT == MIP_BF16 && !VF16;
+
+// Eight bf16 values -> fp16 in place. bf16 has 8 significand bits and fp16 11, so the
+// conversion is exact down to 2^-17 (smaller magnitudes land on fp16's subnormal grid of
+// 2^-24, a change of at most 2^-25) and up to 65280, the largest bf16 value below 65536.
+// Returns whether some value has a magnitude of 65536 or more, or is inf or NaN: bf16 bits
+// 0x4780 and up, which adding 0x3880 to the 15-bit magnitude carries into bit 15.
+__device__ __forceinline__ bool bf16x8_to_f16x8(uint4& v) {
+  constexpr uint32_t kMag = 0x7fff7fffu, kAdd = 0x38803880u;
+  const uint32_t big = ((v.x & kMag) + kAdd) | ((v.y & kMag) + kAdd) | ((v.z & kMag) + kAdd) | ((v.w & kMag) + kAdd);
+  auto cv = [](uint32_t x) __attribute__((always_inline)) {
+    return MfmaOps<MIP_F16>::pack2(__uint_as_float(x << 16), __uint_as_float(x & 0xffff0000u));
+  };
+  v = make_uint4(cv(v.x), cv(v.y), cv(v.z), cv(v.w));
+  return (big & 0x80008000u) != 0;
+}
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane j supplies 4 consecutive 16-bit
 // elements A[j][0..3]; lane i receives A[i / 4][i % 4], A[4 + i / 4][i % 4],
@@ -121,16 +139,21 @@ struct PShape {
 // s_wok[stage] whether every key row wavefront w loaded is. Called by the whole workgroup
 // (the barriers inside are workgroup-wide).
 // q0, n_s and start are cu_q[s], cu_q[s + 1] - cu_q[s] and ctx_start[s] (the caller reads them).
-template <int DT, int D, int NC>
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int s, int q0, int n_s, int start_in,
-                                             int tok_lo, int tok_end, char* smem, uint8_t (*s_ok)[kKT],
-                                             uint32_t* s_wok) {
+// VF16 (bf16 only): V is converted to fp16 as it is staged, and a thread whose V chunk fp16
+// cannot hold stores tag in *s_big; the item then writes nothing and returns true, and the
+// caller runs it again without VF16. tag differs between the items a workgroup runs.
+template <int DT, int D, int NC, bool VF16>
+__device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int kvh, int s, int q0, int n_s, int start_in,
+                                             int tok_lo, int tok_end, uint32_t tag, char* smem,
+                                             uint8_t (*s_ok)[kKT], uint32_t* s_wok, uint32_t* s_big) {
+  static_assert(!VF16 || DT == MIP_BF16, "V is converted from bf16 only");
   using P = PShape<D>;
-  using Ops = MfmaOps<DT>;
+  using Ops = MfmaOps<DT>;                     // Q, K and the output
+  using OpsV = MfmaOps<VF16 ? MIP_F16 : DT>;  // V and P
   constexpr int RB = P::RB, CPR = P::CPR, KC = P::KC, MT = P::MT;
   const int TQ = kPW * NC * 16 / a.group;  // token capacity of the item's rows
 
-  if (tok_lo >= n_s) return;
+  if (tok_lo >= n_s) return false;
   const int tok_hi = tok_end < n_s ? tok_end : n_s;
   const int start = start_in > 0 ? start_in : 0;
   const int cap = a.max_blocks * a.bs;
@@ -219,13 +242,19 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
   };
   auto stash = [&](int stage) __attribute__((always_inline)) {
     char* st = smem + stage * P::STAGE;
+    bool big = false;
 #pragma unroll
     for (int j = 0; j < P::NLD; ++j) {
       const int idx = tid + j * kPW * kWave;
       const int r = idx / CPR, c = idx % CPR;
+      uint4 vv = vbuf[j];
+      if constexpr (VF16) big = bf16x8_to_f16x8(vv) || big;
       *reinterpret_cast<uint4*>(st + r * RB + ((c ^ (r & (CPR - 1))) * 16)) = kbuf[j];  // K swizzled by row
-      *reinterpret_cast<uint4*>(st + P::TILE + r * RB + ((c ^ P::vsw(r)) * 16)) = vbuf[j];
+      *reinterpret_cast<uint4*>(st + P::TILE + r * RB + ((c ^ P::vsw(r)) * 16)) = vv;
       if (c == 0) s_ok[stage][r] = okbuf[j];
+    }
+    if constexpr (VF16) {
+      if (big) *s_big = tag;
     }
     bool wok = true;
 #pragma unroll
@@ -360,17 +389,17 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
 #pragma unroll
         for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(fmaf(sv[c][i], a.scale_log2, nm[c]));
         uint4 ph;
-        ph.x = Ops::pack2(pr[0], pr[1]);
-        ph.y = Ops::pack2(pr[2], pr[3]);
-        ph.z = Ops::pack2(pr[4], pr[5]);
-        ph.w = Ops::pack2(pr[6], pr[7]);
+        ph.x = OpsV::pack2(pr[0], pr[1]);
+        ph.y = OpsV::pack2(pr[2], pr[3]);
+        ph.z = OpsV::pack2(pr[4], pr[5]);
+        ph.w = OpsV::pack2(pr[6], pr[7]);
         // Row sums of the weights the PV product uses, on the matrix cores.
-        constexpr uint32_t kOne2 = DT == MIP_BF16 ? 0x3f803f80u : 0x3c003c00u;
+        constexpr uint32_t kOne2 = DT == MIP_BF16 && !VF16 ? 0x3f803f80u : 0x3c003c00u;
         const uint4 ones = make_uint4(kOne2, kOne2, kOne2, kOne2);
-        lacc[c] = Ops::qk(ones, ph, lacc[c]);
+        lacc[c] = OpsV::qk(ones, ph, lacc[c]);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[c][mt] = Ops::qk(vt[mt], ph, acc[c][mt]);
-        if constexpr (kSplitP<DT>) {
+        for (int mt = 0; mt < MT; ++mt) acc[c][mt] = OpsV::qk(vt[mt], ph, acc[c][mt]);
+        if constexpr (kSplitP<DT, VF16>) {
           // bf16 keeps only 8 bits of p: add the rounding remainder as a second product.
           uint4 pl;
           pl.x = Ops::pack2(pr[0] - Ops::lo(ph.x), pr[1] - Ops::hi(ph.x));
@@ -386,6 +415,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
     }
     if (t + 1 < n_tiles) stash(stage ^ 1);
     __syncthreads();
+  }
+  if constexpr (VF16) {
+    const bool redo = __builtin_amdgcn_readfirstlane(*s_big) == tag;
+    // Every thread reads the flag before any stages the next item (which may store to it).
+    __syncthreads();
+    if (redo) return true;
   }
 
   // ---- normalise and write each live row: lane (row i16, group grp) holds d = 16 mt + 4 grp + 0..3.
@@ -407,6 +442,30 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int kvh, int 
       *reinterpret_cast<uint2*>(orow + 16 * mt + 4 * grp) = make_uint2(w0, w1);
     }
   }
+  return false;
+}
+
+struct ItemArgs {
+  int kvh, s, q0, n_s, start, tok_lo, tok_end;
+};
+
+// One work item, as prefill_item describes: bf16 items at head_dim 64 with V staged as fp16
+// first, and again with bf16 V where that finds a value fp16 cannot hold (at head_dim 128 the
+// conversion's registers would spill inside the tile loop, so those items split P). args()
+// yields the item's arguments; it is called again for the second pass, so nothing but what
+// args() reads stays live across the first.
+template <int DT, int D, int NC, class Args>
+__device__ __forceinline__ void run_item(const PrefillArgs& a, const Args& args, uint32_t tag, char* smem,
+                                         uint8_t (*s_ok)[kKT], uint32_t* s_wok, uint32_t* s_big) {
+  if constexpr (DT == MIP_BF16 && D == 64) {
+    const ItemArgs x = args();
+    if (!prefill_item<DT, D, NC, true>(a, x.kvh, x.s, x.q0, x.n_s, x.start, x.tok_lo, x.tok_end, tag, smem, s_ok,
+                                       s_wok, s_big))
+      return;
+  }
+  const ItemArgs x = args();
+  prefill_item<DT, D, NC, false>(a, x.kvh, x.s, x.q0, x.n_s, x.start, x.tok_lo, x.tok_end, tag, smem, s_ok, s_wok,
+                                 s_big);
 }
 
 // Work list of the persistent kernel, built in LDS by every workgroup from cu_q: sequences
@@ -426,13 +485,20 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
   __shared__ __attribute__((aligned(16))) char smem[2 * P::STAGE];
   __shared__ uint8_t s_ok[2][kKT];
   __shared__ uint32_t s_wok[2];
+  __shared__ uint32_t s_big;  // tag of the item whose V fp16 cannot hold (bf16 only)
   static_assert(kPW == 4, "one byte per wavefront in s_wok");
   if constexpr (!PERSIST) {
     // One workgroup per (kv head, sequence, block), blocks of a sequence latest first.
-    const int blk = gridDim.z - 1 - blockIdx.z, s = blockIdx.y;
-    const int q0 = a.cu_q[s];
-    prefill_item<DT, D, NC>(a, blockIdx.x, s, q0, a.cu_q[s + 1] - q0, a.ctx_start[s], blk * TQ, blk * TQ + TQ, smem,
-                            s_ok, s_wok);
+    if constexpr (DT == MIP_BF16 && D == 64) {
+      if (threadIdx.x == 0) s_big = 0;
+      __syncthreads();
+    }
+    auto args = [&]() __attribute__((always_inline)) {
+      const int blk = gridDim.z - 1 - blockIdx.z, s = blockIdx.y;
+      const int q0 = a.cu_q[s];
+      return ItemArgs{static_cast<int>(blockIdx.x), s, q0, a.cu_q[s + 1] - q0, a.ctx_start[s], blk * TQ, blk * TQ + TQ};
+    };
+    run_item<DT, D, NC>(a, args, 1u, smem, s_ok, s_wok, &s_big);
   } else {
     __shared__ int s_cu[kMaxSeqs + 1];      // cu_q
     __shared__ int s_st[kMaxSeqs];          // ctx_start
@@ -486,7 +552,10 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
         if (k < zb) s_ipre[k + 1] = incl;
         carry = __shfl(incl, kWave - 1);
       }
-      if (lane == 0) s_ipre[0] = 0;
+      if (lane == 0) {
+        s_ipre[0] = 0;
+        s_big = 0;
+      }
     }
     __syncthreads();
     const int total = s_ipre[zb];
@@ -510,11 +579,17 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
     // the longest of its half.
     const int G = gridDim.x, wg = static_cast<int>(blockIdx.x), H = G / 2;
     const int full = total / G, last = total - full * G;
+    // The arguments of whole item it.
+    auto whole = [&](int it) __attribute__((always_inline)) {
+      return [&, it]() __attribute__((always_inline)) {
+        int seq, kvh, blk;
+        item(it, seq, kvh, blk);
+        return ItemArgs{kvh, seq, s_cu[seq], s_cu[seq + 1] - s_cu[seq], s_st[seq], blk * TQ, blk * TQ + TQ};
+      };
+    };
     for (int r = 0; r < full; ++r) {
-      int seq, kvh, blk;
-      item(r * G + ((r & 1) && wg >= H ? G - 1 - (wg - H) : wg), seq, kvh, blk);
-      prefill_item<DT, D, NC>(a, kvh, seq, s_cu[seq], s_cu[seq + 1] - s_cu[seq], s_st[seq], blk * TQ, blk * TQ + TQ,
-                              smem, s_ok, s_wok);
+      const int it = r * G + ((r & 1) && wg >= H ? G - 1 - (wg - H) : wg);
+      run_item<DT, D, NC>(a, whole(it), it + 1u, smem, s_ok, s_wok, &s_big);
     }
     if (last == 0) return;
     // The last, partial round holds the shortest items (or, in a call of fewer items than
@@ -529,19 +604,22 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
     const int tq2 = NC2 > 0 ? kPW * NC2 * 16 / a.group : 0;
     const int n_split = NC2 > 0 && 2 * tq2 >= TQ ? (last < G - last ? last : G - last) : 0;
     if (u >= last + n_split) return;
-    int seq, kvh, blk;
     if (u < 2 * n_split) {
       if constexpr (NC2 > 0) {
-        item(full * G + u / 2, seq, kvh, blk);
-        const int t0 = blk * TQ + (u & 1) * tq2, t_end = blk * TQ + TQ;
-        prefill_item<DT, D, (NC2 > 0 ? NC2 : 1)>(a, kvh, seq, s_cu[seq], s_cu[seq + 1] - s_cu[seq], s_st[seq], t0,
-                                                   t0 + tq2 < t_end ? t0 + tq2 : t_end, smem, s_ok, s_wok);
+        const int it = full * G + u / 2;
+        auto half = [&]() __attribute__((always_inline)) {
+          int seq, kvh, blk;
+          item(it, seq, kvh, blk);
+          const int t0 = blk * TQ + (u & 1) * tq2, t_end = blk * TQ + TQ;
+          return ItemArgs{kvh, seq, s_cu[seq], s_cu[seq + 1] - s_cu[seq], s_st[seq], t0,
+                          t0 + tq2 < t_end ? t0 + tq2 : t_end};
+        };
+        run_item<DT, D, (NC2 > 0 ? NC2 : 1)>(a, half, it + 1u, smem, s_ok, s_wok, &s_big);
       }
       return;
     }
-    item(full * G + u - n_split, seq, kvh, blk);
-    prefill_item<DT, D, NC>(a, kvh, seq, s_cu[seq], s_cu[seq + 1] - s_cu[seq], s_st[seq], blk * TQ, blk * TQ + TQ, smem,
-                            s_ok, s_wok);
+    const int it = full * G + u - n_split;
+    run_item<DT, D, NC>(a, whole(it), it + 1u, smem, s_ok, s_wok, &s_big);
   }
 }
 

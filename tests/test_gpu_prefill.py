@@ -30,8 +30,9 @@ def half_ulp(x: np.ndarray, dtype: str) -> np.ndarray:
     return 0.5 * np.exp2(np.floor(np.log2(ax)) - MANTISSA_BITS[dtype])
 
 
-def build(gpu, dtype, d, hq, hkv, bs, starts, lengths, seed=0, stale_nan=False, extra_blocks=3):
-    """Scattered pool holding every sequence's keys 0..end-1; padded int32 tables; packed q."""
+def build(gpu, dtype, d, hq, hkv, bs, starts, lengths, seed=0, stale_nan=False, extra_blocks=3, edit_v=None):
+    """Scattered pool holding every sequence's keys 0..end-1; padded int32 tables; packed q.
+    edit_v(v_pool, tables), if given, changes the host V pool before it is copied and checked."""
     rnd = random.Random(seed)
     ends = [a + n for a, n in zip(starts, lengths)]
     need = [(e + bs - 1) // bs for e in ends]
@@ -51,6 +52,8 @@ def build(gpu, dtype, d, hq, hkv, bs, starts, lengths, seed=0, stale_nan=False, 
             last, used = t[-1], e - (len(t) - 1) * bs
             k_pool[last, :, used:] = float("nan")
             v_pool[last, :, used:] = float("nan")
+    if edit_v is not None:
+        edit_v(v_pool, tables)
     # q as the packed [N, Hq, D] view of a wider qkv row, like the model's projection output.
     n_all = sum(lengths)
     qkv = torch.randn(n_all, (hq + 2 * hkv) * d, generator=g).to(dt)
@@ -320,6 +323,52 @@ def test_paged_prefill_persistent_limits(gpu):
 
     announce("paged_prefill one sequence of 9180 new tokens after 100 cached (persistent grid, 255 blocks)")
     _long_sequence_rows(gpu, rnd, 100, 255 * 36, seed=31, dtype="float16")
+
+
+# bf16 V at head_dim 64 is staged as fp16 (exact up to 65280, the largest bf16 value below
+# 65536); an item whose V holds a larger magnitude runs again with bf16 V and a split P.
+# (planted values, sequences (starts, lengths)): the largest values that convert; values that
+# force the second pass, in one sequence of several and in many; the per-item grid (1100
+# sequences) with values that force it.
+_RND = random.Random(41)
+BF16_RANGE_CASES = [
+    ([65280.0, -65280.0], ([37, 0, 512, 3], [5, 33, 100, 1])),
+    ([1.0e5, -3.0e4], ([37, 0, 512, 3], [5, 33, 100, 1])),
+    ([1.0e30, -7.0e5, 70000.0], ([_RND.randint(0, 300) for _ in range(40)], [_RND.randint(1, 200) for _ in range(40)])),
+    ([2.0e5, -65536.0], ([_RND.randint(0, 40) for _ in range(1100)], [_RND.randint(1, 3) for _ in range(1100)])),
+]
+
+
+@pytest.mark.parametrize("case", range(len(BF16_RANGE_CASES)))
+def test_paged_prefill_bf16_values_beyond_fp16(gpu, case):
+    """Values near and beyond fp16's range in a bf16 V pool, against float64: every output
+    finite, and within 2e-3 + 2^-11 M beyond half an ulp, M the largest planted magnitude
+    (P is rounded to 16 bits, 2^-11 relative at fp16, which moves an output by at most
+    2^-11 times the values' spread; the 2e-3 bound is for values of unit scale)."""
+    from engine import paged_ops
+
+    values, (starts, lengths) = BF16_RANGE_CASES[case]
+    rnd = random.Random(100 + case)
+    d, hq, hkv, bs = 64, 14, 2, 16
+    # Only the first of several sequences gets the planted values, unless there is just one
+    # kind of case to show (many sequences: spread over all of them).
+    few = len(lengths) <= 4
+
+    def plant(v_pool, tables):
+        chosen = tables[:1] if few else tables
+        for i in range(24):
+            t = rnd.choice(chosen)
+            v_pool[rnd.choice(t), rnd.randrange(hkv), rnd.randrange(bs), rnd.randrange(d)] = values[i % len(values)]
+
+    announce(f"paged_prefill bf16 V values {values}, {len(lengths)} sequences")
+    dev, want = build(gpu, "bfloat16", d, hq, hkv, bs, starts, lengths, seed=200 + case, edit_v=plant)
+    out = paged_ops.paged_prefill(dev["q"], dev["k"], dev["v"], dev["tab"], dev["cu"], dev["st"], max(lengths))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert np.abs(want).max() > 1000.0  # some planted value reaches an output
+    err = float((np.abs(got - want) - half_ulp(want, "bfloat16")).max())
+    assert err <= TOL["bfloat16"] + 2.0 ** -11 * max(abs(x) for x in values), err
 
 
 # Work lists whose last, partial round of the persistent grid takes each form on a device of
