@@ -281,9 +281,10 @@ def decode_tok_s(batch, steps: int, warmup: int) -> dict:
             "eager_attend_ms_per_step": t_eager_attend * 1e3, "steps": steps}
 
 
-def prefill_measure(dev, iters: int = 30) -> dict:
+def prefill_measure(dev, iters: int = 30, dtype: str = "float16") -> dict:
     """Packed prefill attention of the shared-prefix workload (64 forks of a 520-token cached
-    prefix, suffixes U[32, 512], fp16, 14q/2kv heads d64, block 16), one layer, HIP events.
+    prefix, suffixes U[32, 512], fp16 or bf16, 14q/2kv heads d64, block 16), one layer, HIP
+    events.
 
     The new tokens attend their sequence's cached prefix and their own earlier tokens through
     the paged prefill kernel (``mip_paged_prefill``); flops = 4 * D * Hq * sum(position + 1).
@@ -292,12 +293,14 @@ def prefill_measure(dev, iters: int = 30) -> dict:
 
     from engine import paged_ops, workloads
 
-    pb = workloads.build_prefix_batch(dev, seed=0, num_layers=1)
+    dt = getattr(torch, dtype)
+    short = {"float16": "fp16", "bfloat16": "bf16"}[dtype]
+    pb = workloads.build_prefix_batch(dev, seed=0, num_layers=1, dtype=dt)
     ctx = pb.cache.packed_prefill_context(pb.children, pb.suffix_lens)  # appends nothing; CoW of the shared block
     hq, d = 14, 64
     n = sum(pb.suffix_lens)
     gen = torch.Generator(device=dev).manual_seed(7)
-    q = torch.randn(n, hq, d, generator=gen, device=dev).half()
+    q = torch.randn(n, hq, d, generator=gen, device=dev).to(dt)
     out = torch.empty_like(q)
     k_layer, v_layer = pb.cache.k[0], pb.cache.v[0]
 
@@ -322,9 +325,10 @@ def prefill_measure(dev, iters: int = 30) -> dict:
     tflops = 4 * d * hq * keys / t / 1e12
     return {
         "workload": f"packed prefill attention over a cached prefix: {len(pb.children)} forks of a "
-                    f"{pb.prefix_len}-token prefix + suffixes U[32,512] ({n} new tokens), fp16, 14q/2kv heads d64, "
+                    f"{pb.prefix_len}-token prefix + suffixes U[32,512] ({n} new tokens), {short}, 14q/2kv heads d64, "
                     "block 16, one layer",
-        "kernel": "paged_prefill_kernel<f16, D=64, NC=4> (query rows packed as (token, head) pairs, 36 tokens per workgroup)",
+        "kernel": f"paged_prefill_kernel<{'f16' if short == 'fp16' else 'bf16'}, D=64, NC=4> (query rows packed as "
+                  "(token, head) pairs, 36 tokens per workgroup" + ("; V staged as fp16)" if short == "bf16" else ")"),
         "us_per_layer": round(t * 1e6, 1),
         "us_per_layer_cold": round(t_cold * 1e6, 1),
         "timing": "HIP events over 30 calls after 0.1 s of back-to-back calls (sustained clocks); "
@@ -745,6 +749,12 @@ def main() -> int:
             pf = result["prefill"]
             log(f"prefill attention: {pf['us_per_layer']} us/layer sustained, {pf['achieved']} TFLOP/s ({pf['frac']:.1%} of "
                 f"peak); {pf['us_per_layer_cold']} us/layer right after the other legs")
+            # The same workload in bf16, right after the fp16 figure (so at the clocks that one
+            # raised: only its sustained figure is reported).
+            pb16 = prefill_measure(dev, dtype="bfloat16")
+            pf["bf16"] = {k: pb16[k] for k in ("kernel", "us_per_layer", "achieved", "frac")}
+            log(f"prefill attention bf16: {pb16['us_per_layer']} us/layer sustained, {pb16['achieved']} TFLOP/s "
+                f"({pb16['frac']:.1%} of peak)")
         except Exception as exc:
             log(f"prefill measurement failed: {exc!r}")
             result["prefill"] = None
