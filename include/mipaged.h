@@ -279,10 +279,10 @@ int mip_paged_decode_plan(const int32_t* context_lens, const int32_t* block_tabl
  * (group = num_heads / num_kv_heads), i.e. each new token sees its sequence's cached prefix
  * and its own sequence's new tokens up to itself; every key it reads must already be in the
  * pool (append first). Scores, sums and products accumulate in fp32; on the MFMA kernel the
- * softmax weights enter the V product rounded to fp16 (2^-11 relative): bf16 V at head_dim 64
- * is staged as fp16 (exact below 65536 in magnitude), and an item whose V holds a larger value,
- * inf or NaN, like bf16 at head_dim 128, uses bf16 V with each weight split into two bf16
- * parts. The output is rounded once to dtype. Keys past
+ * softmax weights enter the V product rounded to fp16 (2^-11 relative): bf16 V is staged as
+ * fp16 (exact below 65536 in magnitude), and an item whose V holds a larger value, inf or NaN
+ * uses bf16 V with each weight split into two bf16 parts. The output is rounded once to
+ * dtype. Keys past
  * max_blocks_per_seq * block_size are never read (positions beyond are clamped to the last
  * one). max_q_len must be >= every cu_q[s + 1] - cu_q[s]; it only sizes the grid, which
  * depends on the integer arguments alone.

@@ -449,15 +449,14 @@ struct ItemArgs {
   int kvh, s, q0, n_s, start, tok_lo, tok_end;
 };
 
-// One work item, as prefill_item describes: bf16 items at head_dim 64 with V staged as fp16
-// first, and again with bf16 V where that finds a value fp16 cannot hold (at head_dim 128 the
-// conversion's registers would spill inside the tile loop, so those items split P). args()
-// yields the item's arguments; it is called again for the second pass, so nothing but what
-// args() reads stays live across the first.
+// One work item, as prefill_item describes: bf16 items with V staged as fp16 first, and again
+// with bf16 V where that finds a value fp16 cannot hold. args() yields the item's arguments;
+// it is called again for the second pass, so nothing but what args() reads stays live across
+// the first.
 template <int DT, int D, int NC, class Args>
 __device__ __forceinline__ void run_item(const PrefillArgs& a, const Args& args, uint32_t tag, char* smem,
                                          uint8_t (*s_ok)[kKT], uint32_t* s_wok, uint32_t* s_big) {
-  if constexpr (DT == MIP_BF16 && D == 64) {
+  if constexpr (DT == MIP_BF16) {
     const ItemArgs x = args();
     if (!prefill_item<DT, D, NC, true>(a, x.kvh, x.s, x.q0, x.n_s, x.start, x.tok_lo, x.tok_end, tag, smem, s_ok,
                                        s_wok, s_big))
@@ -489,7 +488,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
   static_assert(kPW == 4, "one byte per wavefront in s_wok");
   if constexpr (!PERSIST) {
     // One workgroup per (kv head, sequence, block), blocks of a sequence latest first.
-    if constexpr (DT == MIP_BF16 && D == 64) {
+    if constexpr (DT == MIP_BF16) {
       if (threadIdx.x == 0) s_big = 0;
       __syncthreads();
     }

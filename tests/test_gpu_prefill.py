@@ -325,17 +325,20 @@ def test_paged_prefill_persistent_limits(gpu):
     _long_sequence_rows(gpu, rnd, 100, 255 * 36, seed=31, dtype="float16")
 
 
-# bf16 V at head_dim 64 is staged as fp16 (exact up to 65280, the largest bf16 value below
-# 65536); an item whose V holds a larger magnitude runs again with bf16 V and a split P.
-# (planted values, sequences (starts, lengths)): the largest values that convert; values that
+# bf16 V is staged as fp16 (exact up to 65280, the largest bf16 value below 65536); an item
+# whose V holds a larger magnitude runs again with bf16 V and a split P. (planted values,
+# sequences (starts, lengths), (d, hq, hkv, bs)): the largest values that convert; values that
 # force the second pass, in one sequence of several and in many; the per-item grid (1100
-# sequences) with values that force it.
+# sequences) with values that force it; head_dim 128.
 _RND = random.Random(41)
+_D64 = (64, 14, 2, 16)
 BF16_RANGE_CASES = [
-    ([65280.0, -65280.0], ([37, 0, 512, 3], [5, 33, 100, 1])),
-    ([1.0e5, -3.0e4], ([37, 0, 512, 3], [5, 33, 100, 1])),
-    ([1.0e30, -7.0e5, 70000.0], ([_RND.randint(0, 300) for _ in range(40)], [_RND.randint(1, 200) for _ in range(40)])),
-    ([2.0e5, -65536.0], ([_RND.randint(0, 40) for _ in range(1100)], [_RND.randint(1, 3) for _ in range(1100)])),
+    ([65280.0, -65280.0], ([37, 0, 512, 3], [5, 33, 100, 1]), _D64),
+    ([1.0e5, -3.0e4], ([37, 0, 512, 3], [5, 33, 100, 1]), _D64),
+    ([1.0e30, -7.0e5, 70000.0], ([_RND.randint(0, 300) for _ in range(40)], [_RND.randint(1, 200) for _ in range(40)]),
+     _D64),
+    ([2.0e5, -65536.0], ([_RND.randint(0, 40) for _ in range(1100)], [_RND.randint(1, 3) for _ in range(1100)]), _D64),
+    ([65280.0, 1.0e5], ([37, 0, 512, 3], [5, 33, 100, 1]), (128, 28, 4, 32)),
 ]
 
 
@@ -347,9 +350,8 @@ def test_paged_prefill_bf16_values_beyond_fp16(gpu, case):
     2^-11 times the values' spread; the 2e-3 bound is for values of unit scale)."""
     from engine import paged_ops
 
-    values, (starts, lengths) = BF16_RANGE_CASES[case]
+    values, (starts, lengths), (d, hq, hkv, bs) = BF16_RANGE_CASES[case]
     rnd = random.Random(100 + case)
-    d, hq, hkv, bs = 64, 14, 2, 16
     # Only the first of several sequences gets the planted values, unless there is just one
     # kind of case to show (many sequences: spread over all of them).
     few = len(lengths) <= 4
