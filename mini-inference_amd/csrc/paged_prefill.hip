@@ -87,23 +87,19 @@ __device__ __forceinline__ float max4(float x) {
 // the 2e-3 bound on outputs that are convex combinations of the values; bf16 (2^-8) is not.
 // bf16 items therefore first run with V converted to fp16 as it is staged (bf16x8_to_f16x8:
 // exact for every value fp16 can hold), so P stays fp16 and the PV product is one fp16
-// MFMA; an item whose staged V holds a value fp16 cannot (|v| >= 65536, inf, NaN) runs again
-// with bf16 V and P split into a rounded part and its remainder, each multiplied by V^T.
+// MFMA; an item that meets a value fp16 cannot hold (|v| >= 65536, inf, NaN) runs again with
+// bf16 V and P split into a rounded part and its remainder, each multiplied by V^T.
 template <int DT, bool VF16> constexpr bool kSplitP = DT == MIP_BF16 && !VF16;
 
 // Eight bf16 values -> fp16 in place. bf16 has 8 significand bits and fp16 11, so the
 // conversion is exact down to 2^-17 (smaller magnitudes land on fp16's subnormal grid of
-// 2^-24, a change of at most 2^-25) and up to 65280, the largest bf16 value below 65536.
-// Returns whether some value has a magnitude of 65536 or more, or is inf or NaN: bf16 bits
-// 0x4780 and up, which adding 0x3880 to the 15-bit magnitude carries into bit 15.
-__device__ __forceinline__ bool bf16x8_to_f16x8(uint4& v) {
-  constexpr uint32_t kMag = 0x7fff7fffu, kAdd = 0x38803880u;
-  const uint32_t big = ((v.x & kMag) + kAdd) | ((v.y & kMag) + kAdd) | ((v.z & kMag) + kAdd) | ((v.w & kMag) + kAdd);
+// 2^-24, a change of at most 2^-25) and up to 65280, the largest bf16 value below 65536;
+// 65536 and more become inf (round to nearest even), inf and NaN stay what they are.
+__device__ __forceinline__ void bf16x8_to_f16x8(uint4& v) {
   auto cv = [](uint32_t x) __attribute__((always_inline)) {
     return MfmaOps<MIP_F16>::pack2(__uint_as_float(x << 16), __uint_as_float(x & 0xffff0000u));
   };
   v = make_uint4(cv(v.x), cv(v.y), cv(v.z), cv(v.w));
-  return (big & 0x80008000u) != 0;
 }
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane j supplies 4 consecutive 16-bit
@@ -139,9 +135,13 @@ struct PShape {
 // s_wok[stage] whether every key row wavefront w loaded is. Called by the whole workgroup
 // (the barriers inside are workgroup-wide).
 // q0, n_s and start are cu_q[s], cu_q[s + 1] - cu_q[s] and ctx_start[s] (the caller reads them).
-// VF16 (bf16 only): V is converted to fp16 as it is staged, and a thread whose V chunk fp16
-// cannot hold stores tag in *s_big; the item then writes nothing and returns true, and the
-// caller runs it again without VF16. tag differs between the items a workgroup runs.
+// VF16 (bf16 only): V is converted to fp16 as it is staged. A V value fp16 cannot hold is inf
+// there, and the PV product multiplies every key of a tile into every row of the wavefront
+// (0 * inf = NaN), so a wavefront that reached such a key holds a non-finite accumulator; a
+// wavefront that did not has no row that sees it. A wavefront with a non-finite accumulator
+// stores tag in *s_big; the item then writes nothing and returns true, and the caller runs it
+// again without VF16 (so do items whose inputs are inf or NaN). tag differs between the items
+// a workgroup runs.
 template <int DT, int D, int NC, bool VF16>
 __device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int kvh, int s, int q0, int n_s, int start_in,
                                              int tok_lo, int tok_end, uint32_t tag, char* smem,
@@ -242,19 +242,15 @@ __device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int kvh, int 
   };
   auto stash = [&](int stage) __attribute__((always_inline)) {
     char* st = smem + stage * P::STAGE;
-    bool big = false;
 #pragma unroll
     for (int j = 0; j < P::NLD; ++j) {
       const int idx = tid + j * kPW * kWave;
       const int r = idx / CPR, c = idx % CPR;
       uint4 vv = vbuf[j];
-      if constexpr (VF16) big = bf16x8_to_f16x8(vv) || big;
+      if constexpr (VF16) bf16x8_to_f16x8(vv);
       *reinterpret_cast<uint4*>(st + r * RB + ((c ^ (r & (CPR - 1))) * 16)) = kbuf[j];  // K swizzled by row
       *reinterpret_cast<uint4*>(st + P::TILE + r * RB + ((c ^ P::vsw(r)) * 16)) = vv;
       if (c == 0) s_ok[stage][r] = okbuf[j];
-    }
-    if constexpr (VF16) {
-      if (big) *s_big = tag;
     }
     bool wok = true;
 #pragma unroll
@@ -417,6 +413,16 @@ __device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int kvh, int 
     __syncthreads();
   }
   if constexpr (VF16) {
+    // maximum() propagates NaN, so mxa < inf fails for any inf or NaN accumulator.
+    float mxa = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        mxa = fmax3(mxa, fmax2(fabsf(acc[c][mt][0]), fabsf(acc[c][mt][1])),
+                    fmax2(fabsf(acc[c][mt][2]), fabsf(acc[c][mt][3])));
+    if (__any(!(mxa < INFINITY)) && lane == 0) *s_big = tag;
+    __syncthreads();
     const bool redo = __builtin_amdgcn_readfirstlane(*s_big) == tag;
     // Every thread reads the flag before any stages the next item (which may store to it).
     __syncthreads();
@@ -484,7 +490,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2, 
   __shared__ __attribute__((aligned(16))) char smem[2 * P::STAGE];
   __shared__ uint8_t s_ok[2][kKT];
   __shared__ uint32_t s_wok[2];
-  __shared__ uint32_t s_big;  // tag of the item whose V fp16 cannot hold (bf16 only)
+  __shared__ uint32_t s_big;  // tag of an item to run again with bf16 V (bf16 only)
   static_assert(kPW == 4, "one byte per wavefront in s_wok");
   if constexpr (!PERSIST) {
     // One workgroup per (kv head, sequence, block), blocks of a sequence latest first.

@@ -326,7 +326,7 @@ def test_paged_prefill_persistent_limits(gpu):
 
 
 # bf16 V is staged as fp16 (exact up to 65280, the largest bf16 value below 65536); an item
-# whose V holds a larger magnitude runs again with bf16 V and a split P. (planted values,
+# that reaches a larger magnitude runs again with bf16 V and a split P. (planted values,
 # sequences (starts, lengths), (d, hq, hkv, bs)): the largest values that convert; values that
 # force the second pass, in one sequence of several and in many; the per-item grid (1100
 # sequences) with values that force it; head_dim 128.
